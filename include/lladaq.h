@@ -1,0 +1,185 @@
+/*
+ * lladaq.h -- C ABI of liblladaq.so, the MI355X (gfx950) implementation of
+ * LLaDA_Quant's quantized MoE expert path.
+ *
+ * Conventions
+ *   - Every tensor argument is a caller-owned DEVICE pointer to contiguous,
+ *     row-major memory on the current HIP device; sizes are element counts.
+ *   - `stream` is a hipStream_t passed as an opaque pointer (NULL = the
+ *     default stream). Every call is asynchronous with respect to the host
+ *     and ordered on that stream.
+ *   - Every function returns an LQ_* status. On failure lq_last_error()
+ *     returns a thread-local message naming the problem. No C++ exception
+ *     crosses this boundary, and no function allocates device memory:
+ *     lq_moe_forward takes a caller-supplied workspace sized by
+ *     lq_moe_workspace_bytes.
+ *   - dtype codes: LQ_F32, LQ_F16, LQ_BF16 (IEEE binary32, binary16, bfloat16).
+ *
+ * Reference citations are to Ahmed-Hedhili-se/LLaDA_Quant v0.2.0
+ * (src/LLaDA_Quant/...) and to the fused_moe interface it calls
+ * (INFERENCE_REPO_CHANGES.md).
+ */
+#ifndef LLADAQ_H
+#define LLADAQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LQ_ABI_VERSION 1
+
+/* status codes */
+#define LQ_OK 0
+#define LQ_ERR_VALUE 1       /* bad argument; the Python layer raises ValueError   */
+#define LQ_ERR_UNSUPPORTED 2 /* valid but not implemented on this path             */
+#define LQ_ERR_RUNTIME 3     /* a HIP runtime call failed                          */
+
+/* dtype codes */
+#define LQ_F32 0
+#define LQ_F16 1
+#define LQ_BF16 2
+
+/* scale search codes (QuantConfig.scale_search) */
+#define LQ_SCALE_AMAX 0
+#define LQ_SCALE_MSE 1
+
+typedef void *lq_stream_t;
+
+/* Version of this ABI (LQ_ABI_VERSION). */
+int lq_abi_version(void);
+
+/* Thread-local message of the last failed call on this thread. */
+const char *lq_last_error(void);
+
+/*
+ * Pack int4 values (int8 storage, one value per byte) two per byte along the
+ * last axis: element 2i in the low nibble, 2i+1 in the high nibble, two's
+ * complement.  Replaces algorithms/symmetric.py:296-313 (pack_int4).
+ *   q       [rows, k]      int8, values expected in [-8, 7]
+ *   packed  [rows, k/2]    int8
+ *   range_flag  one device int32 the caller zeroes; the kernel stores 1 into
+ *           it if any value lies outside [-8, 7] (the Python layer then
+ *           raises the reference's ValueError).
+ * k must be even.
+ */
+int lq_pack_int4(const int8_t *q, int64_t rows, int64_t k, int8_t *packed,
+                 int32_t *range_flag, lq_stream_t stream);
+
+/*
+ * Inverse of lq_pack_int4 with sign extension of both nibbles.
+ * Replaces algorithms/symmetric.py:316-346 (unpack_int4).
+ *   packed [rows, k_packed] int8  ->  out [rows, 2*k_packed] int8
+ */
+int lq_unpack_int4(const int8_t *packed, int64_t rows, int64_t k_packed,
+                   int8_t *out, lq_stream_t stream);
+
+/*
+ * out = cast(fp32(q) * fp32(scale[row, k / G]), out_dtype), bit-exact to the
+ * reference reconstruction.  Replaces algorithms/symmetric.py:272-293
+ * (dequantize_tensor) and the PACKED property body runtime/moe.py:199-216.
+ *   q      [rows, k] int8 (bits=8) or [rows, k/2] packed int8 (bits=4)
+ *   scale  [rows, ng] in scale_dtype; ng = k/G, or 1 when group_size == -1 or
+ *          G does not divide k (the reference's per-row fallback)
+ *   out    [rows, k] in out_dtype
+ */
+int lq_dequant(const int8_t *q, const void *scale, int scale_dtype,
+               int64_t rows, int64_t k, int bits, int64_t group_size,
+               void *out, int out_dtype, lq_stream_t stream);
+
+/*
+ * Groupwise symmetric quantization of w [rows, k] along its last axis, with
+ * amax or MSE clip-search scales; bits=4 output is packed.
+ * Replaces algorithms/symmetric.py:207-269 (quantize_tensor) together with
+ * :117-119 (_amax_scale) and :122-204 (search_group_scale).
+ *   w       [rows, k] in w_dtype (f32, f16 or bf16)
+ *   q       [rows, k] int8 (bits=8) or [rows, k/2] int8 (bits=4, packed)
+ *   scale   [rows, ng] in scale_dtype
+ * scale_search: LQ_SCALE_AMAX or LQ_SCALE_MSE; grid/max_shrink are the
+ * search's candidate count and clip range (ignored for amax).
+ */
+int lq_quantize(const void *w, int w_dtype, int64_t rows, int64_t k, int bits,
+                int64_t group_size, int scale_search, int grid,
+                double max_shrink, int8_t *q, void *scale, int scale_dtype,
+                lq_stream_t stream);
+
+/*
+ * MSE-optimal per-group scale alone (fp32), for grouped weights viewed as
+ * [n_groups, group_len].  Replaces algorithms/symmetric.py:122-204
+ * (search_group_scale).
+ */
+int lq_search_group_scale(const void *w, int w_dtype, int64_t n_groups,
+                          int64_t group_len, int bits, int grid,
+                          double max_shrink, float *scale, lq_stream_t stream);
+
+/*
+ * Router front end: probs = softmax(fp32(logits)), top-k ids ordered by
+ * descending probability (ties: lower expert id first), their probabilities
+ * as weights, renormalized to sum 1 when `renormalize` != 0.
+ * Replaces the routing in TritonFusedMoEBlock.forward, restated at
+ * trajectory/llada.py:228-234 (softmax(gate(x), fp32).topk(k)).
+ *   logits [T, E] in logits_dtype (f32 or bf16); ids [T, k] int32;
+ *   weights [T, k] f32.  1 <= k <= E <= 256.
+ */
+int lq_route_topk(const void *logits, int logits_dtype, int64_t T, int E,
+                  int k, int renormalize, int32_t *topk_ids,
+                  float *topk_weights, lq_stream_t stream);
+
+/*
+ * weights[t, j] = probs[t, ids[t, j]] (optionally renormalized), for callers
+ * that hand fused_moe a gating_output of softmax probabilities plus topk_ids
+ * (INFERENCE_REPO_CHANGES.md:110-111).  ids are int32 (ids_int64 == 0) or
+ * int64 (ids_int64 != 0); ids32_out receives them as int32.
+ */
+int lq_gather_topk_weights(const float *probs, const void *ids, int ids_int64,
+                           int64_t T, int E, int k, int renormalize,
+                           int32_t *ids32_out, float *topk_weights,
+                           lq_stream_t stream);
+
+/*
+ * Stable expert permutation of the T*k assignments (flat index a = t*k + j):
+ *   counts[e]     number of assignments routed to expert e
+ *   offsets[e]    exclusive prefix of counts (offsets[E] = T*k)
+ *   sorted[p]     assignment ids grouped by expert, ascending a within one
+ *                 expert (the bit-identical order of moe_align_block_size,
+ *                 INFERENCE_REPO_CHANGES.md:274-278; counts restate
+ *                 analysis/moe_regime.py:197-213 expert_token_stats)
+ * ids are int32 in [0, E).
+ */
+int lq_moe_permute(const int32_t *topk_ids, int64_t T, int k, int E,
+                   int32_t *counts, int32_t *offsets, int32_t *sorted,
+                   lq_stream_t stream);
+
+/* Bytes of workspace lq_moe_forward needs for this shape. */
+size_t lq_moe_workspace_bytes(int64_t T, int H, int I, int E, int k);
+
+/*
+ * The quantized expert layer (fused_moe with packed weights):
+ *   out[t] = sum_j w[t,j] * W2[e]^T act(W1[e] x[t]),  e = ids[t,j]
+ *   act(g, u) = bf16(bf16(silu(bf16(g))) * bf16(u)), gate = W1[e][:I],
+ *   up = W1[e][I:], weights dequantized in registers as bf16(fp32(q)*s).
+ * Replaces dequantize-then-fused_moe: runtime/moe.py:199-216 feeding
+ * fused_moe(x, w1, w2, gating_output, topk_ids) (INFERENCE_REPO_CHANGES.md:
+ * 37-63, 110-111, 259-265, 296-309).
+ *   x   [T, H] bf16                         out [T, H] bf16
+ *   q1  [E, 2I, H] int8 / [E, 2I, H/2] packed, s1 [E, 2I, H/G] f32
+ *   q2  [E, H, I]  int8 / [E, H, I/2]  packed, s2 [E, H, I/G]  f32
+ *   topk_ids [T, k] int32, topk_weights [T, k] f32
+ *   workspace of ws_bytes >= lq_moe_workspace_bytes(T, H, I, E, k)
+ * Requires H % 128 == 0, I % 64 == 0, and a group size (or the per-row
+ * fallback length) that is a multiple of 32.
+ */
+int lq_moe_forward(const void *x, int64_t T, int H, int I, int E, int k,
+                   const int8_t *q1, const float *s1, const int8_t *q2,
+                   const float *s2, int bits, int64_t group_size,
+                   const int32_t *topk_ids, const float *topk_weights,
+                   void *workspace, size_t ws_bytes, void *out,
+                   lq_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LLADAQ_H */
