@@ -95,13 +95,14 @@ int lq_dequant(const int8_t *q, const void *scale, int scale_dtype,
  * Replaces algorithms/symmetric.py:207-269 (quantize_tensor) together with
  * :117-119 (_amax_scale) and :122-204 (search_group_scale).
  *   w       [rows, k] in w_dtype (f32, f16 or bf16)
- *   q       [rows, k] int8 (bits=8) or [rows, k/2] int8 (bits=4, packed)
+ *   q       [rows, k] int8 (bits=8, or bits=4 with pack=0: one value per
+ *           byte) or [rows, k/2] int8 (bits=4, pack!=0: two per byte)
  *   scale   [rows, ng] in scale_dtype
  * scale_search: LQ_SCALE_AMAX or LQ_SCALE_MSE; grid/max_shrink are the
  * search's candidate count and clip range (ignored for amax).
  */
 int lq_quantize(const void *w, int w_dtype, int64_t rows, int64_t k, int bits,
-                int64_t group_size, int scale_search, int grid,
+                int pack, int64_t group_size, int scale_search, int grid,
                 double max_shrink, int8_t *q, void *scale, int scale_dtype,
                 lq_stream_t stream);
 
@@ -164,19 +165,22 @@ size_t lq_moe_workspace_bytes(int64_t T, int H, int I, int E, int k);
  * fused_moe(x, w1, w2, gating_output, topk_ids) (INFERENCE_REPO_CHANGES.md:
  * 37-63, 110-111, 259-265, 296-309).
  *   x   [T, H] bf16                         out [T, H] bf16
- *   q1  [E, 2I, H] int8 / [E, 2I, H/2] packed, s1 [E, 2I, H/G] f32
- *   q2  [E, H, I]  int8 / [E, H, I/2]  packed, s2 [E, H, I/G]  f32
- *   topk_ids [T, k] int32, topk_weights [T, k] f32
+ *   q1  [E, 2I, H] int8 / [E, 2I, H/2] packed, s1 [E, 2I, H/G1] f32
+ *   q2  [E, H, I]  int8 / [E, H, I/2]  packed, s2 [E, H, I/G2]  f32
+ *   group_w1, group_w2: group lengths G1 (along H) and G2 (along I) as the
+ *           quantizer recorded them for each tensor (-1 = one group per row)
+ *   topk_ids [T, k] int32, topk_weights [T, k] f32; ids outside [0, E)
+ *           contribute nothing
  *   workspace of ws_bytes >= lq_moe_workspace_bytes(T, H, I, E, k)
- * Requires H % 128 == 0, I % 64 == 0, and a group size (or the per-row
- * fallback length) that is a multiple of 32.
+ * Requires H % 128 == 0, I % 64 == 0, and group lengths (after the per-row
+ * fallback) that are multiples of 32.
  */
 int lq_moe_forward(const void *x, int64_t T, int H, int I, int E, int k,
                    const int8_t *q1, const float *s1, const int8_t *q2,
-                   const float *s2, int bits, int64_t group_size,
-                   const int32_t *topk_ids, const float *topk_weights,
-                   void *workspace, size_t ws_bytes, void *out,
-                   lq_stream_t stream);
+                   const float *s2, int bits, int64_t group_w1,
+                   int64_t group_w2, const int32_t *topk_ids,
+                   const float *topk_weights, void *workspace,
+                   size_t ws_bytes, void *out, lq_stream_t stream);
 
 #ifdef __cplusplus
 }

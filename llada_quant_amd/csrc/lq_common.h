@@ -1,0 +1,140 @@
+// lq_common.h -- shared definitions of liblladaq.so (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/lladaq.h"
+
+namespace lq {
+
+// ---------------------------------------------------------------------------
+// error reporting across the C ABI: a thread-local message + status code
+// ---------------------------------------------------------------------------
+void set_error(const std::string &msg);
+int fail(int status, const std::string &msg);
+int check_launch(const char *what);
+
+#define LQ_HIP_CHECK(expr)                                                   \
+  do {                                                                       \
+    hipError_t _e = (expr);                                                  \
+    if (_e != hipSuccess)                                                    \
+      return ::lq::fail(LQ_ERR_RUNTIME, std::string(#expr " failed: ") +     \
+                                            hipGetErrorString(_e));          \
+  } while (0)
+
+inline hipStream_t as_stream(lq_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// the reference's grouping (algorithms/symmetric.py:85-90): G divides k ->
+// groups of G, otherwise (or G == -1) one group spanning the whole row.
+inline int64_t effective_group(int64_t k, int64_t group_size) {
+  if (group_size == -1 || group_size <= 0 || k % group_size != 0) return k;
+  return group_size;
+}
+
+inline bool valid_dtype(int d) { return d == LQ_F32 || d == LQ_F16 || d == LQ_BF16; }
+
+// ---------------------------------------------------------------------------
+// scalar conversions (device)
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// torch's float -> bfloat16 (round half to even, NaN -> 0x7FC0).  Used where
+// the result must equal the reference bit for bit for every input.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+// IEEE round-to-nearest-even float -> half (what c10::Half does).
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+template <int DT>
+__device__ __forceinline__ float load_f32(const void *p, int64_t i);
+template <>
+__device__ __forceinline__ float load_f32<LQ_F32>(const void *p, int64_t i) {
+  return static_cast<const float *>(p)[i];
+}
+template <>
+__device__ __forceinline__ float load_f32<LQ_F16>(const void *p, int64_t i) {
+  return f16_bits_to_f32(static_cast<const uint16_t *>(p)[i]);
+}
+template <>
+__device__ __forceinline__ float load_f32<LQ_BF16>(const void *p, int64_t i) {
+  return bf16_bits_to_f32(static_cast<const uint16_t *>(p)[i]);
+}
+
+template <int DT>
+__device__ __forceinline__ void store_f32(void *p, int64_t i, float v);
+template <>
+__device__ __forceinline__ void store_f32<LQ_F32>(void *p, int64_t i, float v) {
+  static_cast<float *>(p)[i] = v;
+}
+template <>
+__device__ __forceinline__ void store_f32<LQ_F16>(void *p, int64_t i, float v) {
+  static_cast<uint16_t *>(p)[i] = f32_to_f16_bits(v);
+}
+template <>
+__device__ __forceinline__ void store_f32<LQ_BF16>(void *p, int64_t i, float v) {
+  static_cast<uint16_t *>(p)[i] = f32_to_bf16_bits(v);
+}
+
+// value.to(dtype).float(): the rounding a scale goes through when the
+// reference stores it in scale_dtype (algorithms/symmetric.py:244-245).
+template <int DT>
+__device__ __forceinline__ float round_through(float v) {
+  if constexpr (DT == LQ_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(v));
+  if constexpr (DT == LQ_F16) return f16_bits_to_f32(f32_to_f16_bits(v));
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// wavefront helpers (wave64)
+// ---------------------------------------------------------------------------
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// dispatch a runtime dtype code to a template parameter
+#define LQ_DISPATCH_DTYPE(code, NAME, ...)        \
+  switch (code) {                                 \
+    case LQ_F32: {                                \
+      constexpr int NAME = LQ_F32;                \
+      __VA_ARGS__;                                \
+    } break;                                      \
+    case LQ_F16: {                                \
+      constexpr int NAME = LQ_F16;                \
+      __VA_ARGS__;                                \
+    } break;                                      \
+    default: {                                    \
+      constexpr int NAME = LQ_BF16;               \
+      __VA_ARGS__;                                \
+    } break;                                      \
+  }
+
+}  // namespace lq

@@ -1,0 +1,163 @@
+"""``fused_moe`` over packed expert weights: the quantized expert layer in one HIP call.
+
+Drop-in for the inference repository's
+``fused_moe(hidden_states, w1, w2, gating_output, topk_ids, fuse_silu=None)``
+(INFERENCE_REPO_CHANGES.md:109-111) as ``TritonFusedMoEBlock.forward`` calls
+it with ``w1=self.w1, w2=self.w2``.  With a PACKED block those arguments are
+:class:`~llada_quant_amd.runtime.moe.PackedExpertTensor` handles, and this
+function passes their INT4/INT8 codes and fp32 scales straight to
+``lq_moe_forward``: grouped GEMMs that dequantize in registers, the SwiGLU
+activation fused into GEMM1 (the ``SILU_EPILOGUE`` op order,
+INFERENCE_REPO_CHANGES.md:296-309) and the routed-weight scaling plus top-k
+combine fused into GEMM2.  No BF16 copy of a weight is ever written.
+
+``gating_output`` carries the router's softmax probabilities ``[T, E]``; the
+routed weight of slot ``(t, j)`` is ``gating_output[t, topk_ids[t, j]]``,
+renormalized over the k slots when ``renormalize``.  ``topk_weights`` may be
+passed instead.  :func:`moe_layer` runs the router too, from logits.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Tuple, Union
+
+import torch
+
+from ..algorithms.symmetric import QuantResult
+from . import _lib
+from .moe import PackedExpertTensor
+from .routing import gather_topk_weights, route_topk
+
+PackedWeight = Union[PackedExpertTensor, QuantResult]
+
+
+def _unpack_weight(w: PackedWeight, name: str) -> QuantResult:
+    if isinstance(w, PackedExpertTensor):
+        return w.quant_result()
+    if isinstance(w, QuantResult):
+        return w
+    raise TypeError(
+        f"fused_moe consumes packed expert weights: pass block.{name} of a PACKED block "
+        f"(a PackedExpertTensor) or a QuantResult, got {type(w).__name__}"
+    )
+
+
+def workspace_bytes(tokens: int, hidden: int, intermediate: int, num_experts: int, top_k: int) -> int:
+    return int(_lib.load().lq_moe_workspace_bytes(tokens, hidden, intermediate, num_experts, top_k))
+
+
+def fused_moe_packed(
+    x: torch.Tensor,
+    w1: QuantResult,
+    w2: QuantResult,
+    topk_ids: torch.Tensor,
+    topk_weights: torch.Tensor,
+    out: Optional[torch.Tensor] = None,
+    workspace: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """The layer on explicit operands: ``x [T, H]`` bf16, int32 ids and fp32 weights ``[T, k]``."""
+    if x.dim() != 2:
+        raise ValueError(f"x must be [tokens, hidden], got {tuple(x.shape)}")
+    if x.dtype != torch.bfloat16:
+        raise ValueError(f"fused_moe computes in bfloat16; hidden_states are {x.dtype}")
+    T, H = x.shape
+    if len(w1.logical_shape) != 3 or len(w2.logical_shape) != 3:
+        raise ValueError("w1 and w2 must be [experts, 2*intermediate, hidden] and [experts, hidden, intermediate]")
+    E, two_i, h1 = w1.logical_shape
+    E2, h2, I = w2.logical_shape
+    if E != E2 or h1 != H or h2 != H or two_i != 2 * I:
+        raise ValueError(
+            f"inconsistent shapes: x {tuple(x.shape)}, w1 {tuple(w1.logical_shape)}, w2 {tuple(w2.logical_shape)}"
+        )
+    if w1.bits != w2.bits or w1.packed != w2.packed or w1.packed != (w1.bits == 4):
+        raise ValueError("w1 and w2 must share bits, with INT4 packed two per byte")
+    if w1.scale.dtype != torch.float32 or w2.scale.dtype != torch.float32:
+        raise NotImplementedError("fused_moe reads float32 scales (QuantConfig.scale_dtype='float32')")
+    # every operand shape is checked here: the kernels trust them
+    g1 = w1.group_size if (w1.group_size != -1 and H % w1.group_size == 0) else H
+    g2 = w2.group_size if (w2.group_size != -1 and I % w2.group_size == 0) else I
+    kb = 2 if w1.packed else 1
+    expect = {
+        "w1 codes": (tuple(w1.q.shape), (E, 2 * I, H // kb)),
+        "w1 scales": (tuple(w1.scale.shape), (E, 2 * I, H // g1)),
+        "w2 codes": (tuple(w2.q.shape), (E, H, I // kb)),
+        "w2 scales": (tuple(w2.scale.shape), (E, H, I // g2)),
+    }
+    for what, (got, want) in expect.items():
+        if got != want:
+            raise ValueError(f"{what} have shape {got}, expected {want}")
+    if w1.q.dtype != torch.int8 or w2.q.dtype != torch.int8:
+        raise ValueError("packed expert codes must be int8")
+    k = topk_ids.shape[1]
+    if topk_ids.shape[0] != T or topk_weights.shape != topk_ids.shape:
+        raise ValueError("topk_ids / topk_weights must be [tokens, top_k]")
+    xc = x.contiguous()
+    ids = topk_ids.to(torch.int32).contiguous()
+    wts = topk_weights.to(torch.float32).contiguous()
+    q1, s1, q2, s2 = (t.contiguous() for t in (w1.q, w1.scale, w2.q, w2.scale))
+    device = _lib.require_hip(xc, ids, wts, q1, s1, q2, s2)
+    if out is None:
+        out = torch.empty(T, H, dtype=torch.bfloat16, device=device)
+    ws_need = workspace_bytes(T, H, I, E, k)
+    if workspace is None or workspace.numel() < ws_need:
+        workspace = torch.empty(max(ws_need, 1), dtype=torch.uint8, device=device)
+    if T:
+        lib = _lib.load()
+        with torch.cuda.device(device):
+            rc = lib.lq_moe_forward(
+                _lib.ptr(xc), T, H, I, E, k, _lib.ptr(q1), _lib.ptr(s1), _lib.ptr(q2), _lib.ptr(s2), w1.bits, g1, g2,
+                _lib.ptr(ids), _lib.ptr(wts), _lib.ptr(workspace), workspace.numel(), _lib.ptr(out),
+                _lib.stream(device),
+            )
+        _lib.check(rc, "fused_moe")
+    return out
+
+
+def fused_moe(
+    hidden_states: torch.Tensor,
+    w1: PackedWeight,
+    w2: PackedWeight,
+    gating_output: Optional[torch.Tensor],
+    topk_ids: torch.Tensor,
+    fuse_silu: Optional[bool] = None,
+    *,
+    renormalize: bool = False,
+    topk_weights: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Quantized MoE layer output ``[..., H]`` (bf16) for ``hidden_states [..., H]``.
+
+    ``fuse_silu`` is accepted for signature compatibility: the activation is
+    always applied in GEMM1's epilogue with the unfused path's rounding, which
+    the reference documents as bit-identical to the unfused chain.
+    """
+    del fuse_silu
+    q1 = _unpack_weight(w1, "w1")
+    q2 = _unpack_weight(w2, "w2")
+    H = hidden_states.shape[-1]
+    x = hidden_states.reshape(-1, H)
+    if topk_ids.dim() != 2 or topk_ids.shape[0] != x.shape[0]:
+        raise ValueError(f"topk_ids must be [tokens, top_k] with {x.shape[0]} tokens, got {tuple(topk_ids.shape)}")
+    if topk_weights is None:
+        if gating_output is None:
+            raise ValueError("fused_moe needs gating_output (softmax probabilities) or topk_weights")
+        ids, weights = gather_topk_weights(gating_output.reshape(x.shape[0], -1), topk_ids, renormalize)
+    else:
+        ids, weights = topk_ids, topk_weights
+    out = fused_moe_packed(x, q1, q2, ids, weights)
+    return out.reshape(hidden_states.shape)
+
+
+def moe_layer(
+    hidden_states: torch.Tensor,
+    router_logits: torch.Tensor,
+    w1: PackedWeight,
+    w2: PackedWeight,
+    top_k: int,
+    renormalize: bool = False,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Router + quantized experts: returns ``(output [..., H], topk_ids [T, k])``."""
+    ids, weights = route_topk(router_logits, top_k, renormalize)
+    H = hidden_states.shape[-1]
+    out = fused_moe_packed(hidden_states.reshape(-1, H), _unpack_weight(w1, "w1"), _unpack_weight(w2, "w2"),
+                           ids, weights)
+    return out.reshape(hidden_states.shape), ids

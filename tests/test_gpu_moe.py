@@ -1,0 +1,160 @@
+"""GPU parity of the fused quantized MoE layer (lq_moe_forward).
+
+The oracle is the reference path -- dequantize to BF16 (bit-exact), then the
+fused_moe op order with fp64 accumulation (oracle/lq_oracle.c
+oq_moe_forward).  The north-star tolerance applies to the bf16 output:
+
+    max |out - ref| < 2e-2   and   sum|out - ref| / sum|ref| < 5e-3
+
+At full configuration sizes the oracle runs on a sample of tokens: a token's
+output depends only on its own routing, so the sample is an exact check of
+those rows.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import bits_u16
+from llada_quant_amd.algorithms.symmetric import quantize_tensor
+from llada_quant_amd.runtime.fused_moe import fused_moe, fused_moe_packed, moe_layer
+from llada_quant_amd.runtime.routing import route_topk
+from oracle import oracle as O
+from test_gpu_route import zipf_logits
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+MEAN_REL = 5e-3
+
+
+def make_layer(dev, E, H, I, bits, group=128, seed=0, search="amax", grid=16):
+    g = torch.Generator().manual_seed(seed)
+    w1 = (torch.randn(E, 2 * I, H, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    w2 = (torch.randn(E, H, I, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    q1 = quantize_tensor(w1, bits=bits, group_size=group, scale_search=search, search_grid=grid)
+    q2 = quantize_tensor(w2, bits=bits, group_size=group, scale_search=search, search_grid=grid)
+    return q1, q2
+
+
+def oracle_out(x, q1, q2, ids, weights, rows=None):
+    """Reference output (fp32) for token rows `rows` (all when None)."""
+    xs = x if rows is None else x[rows]
+    ids_np = ids.cpu().numpy() if rows is None else ids.cpu().numpy()[rows]
+    w_np = weights.cpu().numpy() if rows is None else weights.cpu().numpy()[rows]
+    d1 = bits_u16(q1.dequantize(torch.bfloat16))
+    d2 = bits_u16(q2.dequantize(torch.bfloat16))
+    return O.moe_forward(bits_u16(xs), d1, d2, ids_np, w_np)
+
+
+def assert_close(out: torch.Tensor, ref: np.ndarray):
+    o = out.float().cpu().numpy().astype(np.float64)
+    r = ref.astype(np.float64)
+    max_abs = np.abs(o - r).max()
+    mean_rel = np.abs(o - r).sum() / np.abs(r).sum()
+    assert max_abs < MAX_ABS, f"max abs error {max_abs:.3e}"
+    assert mean_rel < MEAN_REL, f"mean relative error {mean_rel:.3e}"
+    return max_abs, mean_rel
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("T,k", [(6, 2), (33, 2), (1, 1), (40, 4)])
+def test_tiny_reference_shape(dev, bits, T, k):
+    """The reference's fixture shape: E=4, H=128, I=64, group 64."""
+    q1, q2 = make_layer(dev, 4, 128, 64, bits, group=64, seed=T)
+    g = torch.Generator().manual_seed(100 + T)
+    x = torch.randn(T, 128, generator=g).to(torch.bfloat16).to(dev)
+    ids, w = route_topk(torch.randn(T, 4, generator=g).to(dev), k, renormalize=True)
+    out = fused_moe_packed(x, q1, q2, ids, w)
+    assert_close(out, oracle_out(x, q1, q2, ids, w))
+
+
+def test_c1_plumbing_case(dev):
+    """C1: E=16, H=1024, I=512, INT4 G=128, 256 tokens, top-2 renormalized; both layers."""
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(256, 1024, generator=g).to(torch.bfloat16).to(dev)
+    for layer in range(2):
+        q1, q2 = make_layer(dev, 16, 1024, 512, 4, seed=10 + layer)
+        ids, w = route_topk(torch.randn(256, 16, generator=g).to(dev), 2, renormalize=True)
+        out = fused_moe_packed(x, q1, q2, ids, w)
+        assert_close(out, oracle_out(x, q1, q2, ids, w))
+        x = out
+
+
+def test_c2_int8_sampled(dev):
+    """C2: INT8, E=64, H=2048, I=1024, 512 tokens, top-8 (oracle on 96 sampled tokens)."""
+    q1, q2 = make_layer(dev, 64, 2048, 1024, 8, seed=2)
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(512, 2048, generator=g).to(torch.bfloat16).to(dev)
+    ids, w = route_topk(torch.randn(512, 64, generator=g).to(dev), 8)
+    out = fused_moe_packed(x, q1, q2, ids, w)
+    rows = np.sort(np.random.default_rng(2).choice(512, 96, replace=False))
+    assert_close(out[torch.from_numpy(rows).to(dev)], oracle_out(x, q1, q2, ids, w, rows))
+
+
+def test_c4_zipf_skew_full(dev):
+    """C4: INT4 MSE, 64 tokens, top-8, Zipf(1.1)-skewed routing (empty and hot experts)."""
+    q1, q2 = make_layer(dev, 64, 2048, 1024, 4, seed=4, search="mse", grid=16)
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(64, 2048, generator=g).to(torch.bfloat16).to(dev)
+    ids, w = route_topk(zipf_logits(64, 64, seed=4).to(dev), 8)
+    counts = torch.bincount(ids.reshape(-1).long().cpu(), minlength=64)
+    assert (counts == 0).any() and counts.max() > 16  # the skew really is there
+    out = fused_moe_packed(x, q1, q2, ids, w)
+    assert_close(out, oracle_out(x, q1, q2, ids, w))
+
+
+def test_c3_large_token_count_sampled(dev):
+    """C3: INT4, 4096 tokens, top-8 (~512 rows per expert), oracle on 48 sampled tokens."""
+    q1, q2 = make_layer(dev, 64, 2048, 1024, 4, seed=3)
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(4096, 2048, generator=g).to(torch.bfloat16).to(dev)
+    ids, w = route_topk(torch.randn(4096, 64, generator=g).to(dev), 8)
+    out = fused_moe_packed(x, q1, q2, ids, w)
+    rows = np.sort(np.random.default_rng(3).choice(4096, 48, replace=False))
+    assert_close(out[torch.from_numpy(rows).to(dev)], oracle_out(x, q1, q2, ids, w, rows))
+
+
+def test_all_tokens_on_one_expert(dev):
+    """A hot expert spans many work units; every other expert is empty."""
+    q1, q2 = make_layer(dev, 8, 256, 128, 4, seed=5)
+    T = 200
+    x = torch.randn(T, 256).to(torch.bfloat16).to(dev)
+    ids = torch.full((T, 1), 5, dtype=torch.int32, device=dev)
+    w = torch.rand(T, 1, device=dev)
+    out = fused_moe_packed(x, q1, q2, ids, w)
+    assert_close(out, oracle_out(x, q1, q2, ids, w))
+
+
+def test_output_is_deterministic(dev):
+    q1, q2 = make_layer(dev, 64, 2048, 1024, 4, seed=6)
+    x = torch.randn(512, 2048).to(torch.bfloat16).to(dev)
+    ids, w = route_topk(zipf_logits(512, 64, seed=6).to(dev), 8)
+    a = fused_moe_packed(x, q1, q2, ids, w)
+    b = fused_moe_packed(x, q1, q2, ids, w)
+    assert torch.equal(a, b)
+
+
+def test_fused_moe_signature_and_moe_layer(dev):
+    """fused_moe(x, w1, w2, gating_output, topk_ids) with probabilities == moe_layer from logits."""
+    q1, q2 = make_layer(dev, 16, 256, 128, 8, seed=7)
+    logits = torch.randn(3, 10, 16, device=dev)
+    x = torch.randn(3, 10, 256, device=dev).to(torch.bfloat16)
+    probs = torch.softmax(logits, -1, dtype=torch.float32)
+    topk_ids = probs.topk(4, dim=-1).indices.reshape(-1, 4)
+    out = fused_moe(x, q1, q2, probs.reshape(-1, 16), topk_ids)
+    assert out.shape == x.shape and out.dtype == torch.bfloat16
+    out2, ids2 = moe_layer(x, logits, q1, q2, top_k=4)
+    assert torch.equal(ids2.long(), topk_ids)
+    torch.testing.assert_close(out, out2, rtol=0, atol=2e-3)
+
+
+def test_shape_mismatch_is_rejected_on_the_host(dev):
+    q1, q2 = make_layer(dev, 4, 128, 64, 4, group=64)
+    x = torch.randn(4, 256, device=dev).to(torch.bfloat16)
+    ids = torch.zeros(4, 1, dtype=torch.int32, device=dev)
+    w = torch.ones(4, 1, device=dev)
+    with pytest.raises(ValueError, match="inconsistent shapes"):
+        fused_moe_packed(x, q1, q2, ids, w)
