@@ -1,0 +1,343 @@
+#!/usr/bin/env python3
+"""Benchmark: MoE-layer tokens/s of the packed W4A16 expert path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c4|c3|c2|c1]
+
+A *step* is one quantized MoE layer over one batch: router (softmax top-k
+from logits), stable expert permutation, GEMM1 + SwiGLU, GEMM2 + routed
+weight, top-k combine -- one ``lq_moe_layer`` call (five kernels on one
+stream).  Inputs are resident in HBM before the timed region; weights rotate
+over several independently quantized copies so every step streams its
+weights from HBM rather than from the 256 MB MALL.
+
+Default workload (the north-star target): C4 of BASELINE.json -- 64 experts,
+hidden 2048, intermediate 1024, INT4 group 128 with MSE scales (grid 16),
+64 tokens ~N(0,1), top-8 routing with Zipf(1.1)-skewed router logits.
+
+One JSON line is printed.  Besides the contract fields it carries
+``roofline`` for the dominant kernel (GEMM1: HBM-bound at C4/C2, MFMA-bound
+at C3), timed with HIP events recorded by the library on the kernel's own
+stream inside the timed region, ``cpu_baseline`` (the reference's
+dequantize-then-matmul path on the host CPU, torch, bounded sample) and
+``gpu_dequant_then_gemm`` (the same layer as dequantize-to-BF16 with the HIP
+dequant kernel, then torch BF16 batched GEMMs on the same GPU).
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+MI355X_HBM_GBPS = 8000.0
+MI355X_BF16_TFLOPS = 2500.0
+
+CONFIGS = {
+    "c4": dict(name="C4", tokens=64, bits=4, search="mse", skew=True, renorm=False, bound="hbm"),
+    "c3": dict(name="C3", tokens=4096, bits=4, search="mse", skew=False, renorm=False, bound="mfma"),
+    "c2": dict(name="C2", tokens=512, bits=8, search="amax", skew=False, renorm=False, bound="hbm"),
+    "c1": dict(name="C1", tokens=256, bits=4, search="amax", skew=False, renorm=True, bound="hbm",
+               experts=16, hidden=1024, inter=512, top_k=2),
+}
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--config", choices=sorted(CONFIGS), default="c4")
+    p.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0: enough to exceed 3x the MALL)")
+    p.add_argument("--cpu-seconds", type=float, default=15.0, help="bound on the CPU baseline sample")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-gpu-baseline", action="store_true", help="skip the dequantize-then-GEMM leg")
+    p.add_argument("--seed", type=int, default=0)
+    return p.parse_args()
+
+
+def zipf_logits(torch, T, E, seed, s=1.1):
+    """Router logits ~N(0,1) plus a per-expert bias making expert popularity Zipf(s)."""
+    g = torch.Generator().manual_seed(seed)
+    perm = torch.randperm(E, generator=g)
+    p = torch.arange(1, E + 1, dtype=torch.float64) ** (-s)
+    bias = torch.log(p / p.sum())[perm].float()
+    return torch.randn(T, E, generator=g) + bias
+
+
+class Hip:
+    """The few HIP runtime calls the bench needs (events), from torch's HIP runtime."""
+
+    def __init__(self):
+        self.lib = ctypes.CDLL("libamdhip64.so.7")
+        self.lib.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.lib.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+
+    def event(self):
+        ev = ctypes.c_void_p()
+        rc = self.lib.hipEventCreate(ctypes.byref(ev))
+        if rc != 0:
+            raise RuntimeError(f"hipEventCreate failed ({rc})")
+        return ev
+
+    def elapsed_ms(self, a, b):
+        ms = ctypes.c_float()
+        rc = self.lib.hipEventElapsedTime(ctypes.byref(ms), a, b)
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
+        return ms.value
+
+    def destroy(self, ev):
+        self.lib.hipEventDestroy(ev)
+
+
+def build_workload(torch, cfg, copies, seed, dev):
+    from llada_quant_amd.algorithms.symmetric import quantize_tensor
+
+    E, H, I, k = cfg["experts"], cfg["hidden"], cfg["inter"], cfg["top_k"]
+    layers = []
+    for c in range(copies):
+        g = torch.Generator(device=dev).manual_seed(seed * 1000 + c)
+        w1 = (torch.randn(E, 2 * I, H, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        w2 = (torch.randn(E, H, I, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        q1 = quantize_tensor(w1, bits=cfg["bits"], group_size=128, scale_search=cfg["search"], search_grid=16)
+        q2 = quantize_tensor(w2, bits=cfg["bits"], group_size=128, scale_search=cfg["search"], search_grid=16)
+        layers.append((q1, q2))
+        del w1, w2
+    g = torch.Generator().manual_seed(seed + 7)
+    T = cfg["tokens"]
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    logits = (zipf_logits(torch, T, E, seed + 11) if cfg["skew"] else torch.randn(T, E, generator=g)).to(dev)
+    return layers, x, logits
+
+
+def layer_bytes(cfg, n_active):
+    """Algorithmic HBM bytes of one layer and of its GEMM1 (compulsory traffic, read once)."""
+    E, H, I, k, T = cfg["experts"], cfg["hidden"], cfg["inter"], cfg["top_k"], cfg["tokens"]
+    vb = 0.5 if cfg["bits"] == 4 else 1.0
+    w1 = 2 * I * H * vb + 2 * I * (H // 128) * 4
+    w2 = H * I * vb + H * (I // 128) * 4
+    gemm1 = n_active * w1 + T * H * 2
+    layer = n_active * (w1 + w2) + T * H * 2 + T * H * 2 + T * E * 4 + T * k * 8
+    return int(layer), int(gemm1)
+
+
+def gpu_dequant_then_gemm(torch, cfg, layers, x, logits, steps, warmup):
+    """Same-GPU baseline: dequantize both weights to BF16 (HIP kernel), then torch BF16 bmm."""
+    from llada_quant_amd.algorithms.symmetric import dequantize_tensor
+    import torch.nn.functional as F
+
+    E, H, I, k, T = cfg["experts"], cfg["hidden"], cfg["inter"], cfg["top_k"], cfg["tokens"]
+
+    def step(q1, q2):
+        w1 = dequantize_tensor(q1.q, q1.scale, q1.bits, q1.group_size, torch.bfloat16, packed=q1.packed)
+        w2 = dequantize_tensor(q2.q, q2.scale, q2.bits, q2.group_size, torch.bfloat16, packed=q2.packed)
+        probs = torch.softmax(logits, -1, dtype=torch.float32)
+        wts, ids = probs.topk(k, dim=-1)
+        flat = ids.reshape(-1)
+        order = torch.argsort(flat, stable=True)
+        counts = torch.bincount(flat, minlength=E)
+        mmax = int(counts.max())  # one host sync, like moe_align_block_size's padding
+        offs = torch.cumsum(counts, 0) - counts
+        pos = torch.arange(N, device=x.device) - offs[flat[order]]
+        tok = order // k
+        xt = torch.zeros(E, H, mmax, dtype=torch.bfloat16, device=x.device)
+        xt[flat[order], :, pos] = x[tok]
+        h = torch.bmm(w1, xt)  # [E, 2I, M]; right operand contiguous
+        act = (F.silu(h[:, :I].float()).to(torch.bfloat16).float() * h[:, I:].float()).to(torch.bfloat16)
+        y = torch.bmm(w2, act.contiguous())  # [E, H, M]
+        yt = y[flat[order], :, pos].float() * wts.reshape(-1)[order].unsqueeze(1)
+        out = torch.zeros(T, H, dtype=torch.float32, device=x.device)
+        out.index_add_(0, tok, yt)
+        return out.to(torch.bfloat16)
+
+    N = T * k
+    for i in range(warmup):
+        step(*layers[i % len(layers)])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(*layers[i % len(layers)])
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    return {"value": round(T * steps / dt, 1), "unit": "tokens/s", "ms_per_step": round(dt / steps * 1e3, 4),
+            "what": "HIP dequant of full w1/w2 to BF16 + torch BF16 bmm over all experts (padded to the "
+                    "max tokens per expert) + SwiGLU + weighted index_add"}
+
+
+def cpu_baseline(torch, cfg, layers, x, logits, budget_s):
+    """The reference's PACKED layer (dequantize-then-matmul) on the host CPU, bounded sample."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import torch_ref
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    q1, q2 = layers[0]
+    args = [t.cpu() for t in (x, logits.float(), q1.q, q1.scale, q2.q, q2.scale)]
+    torch_ref.packed_layer(*args, cfg["bits"], 128, cfg["top_k"], cfg["renorm"])  # warm
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        torch_ref.packed_layer(*args, cfg["bits"], 128, cfg["top_k"], cfg["renorm"])
+        steps += 1
+        dt = time.perf_counter() - t0
+        if dt >= budget_s or steps >= 50:
+            break
+    cpu_model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(cfg["tokens"] * steps / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{steps} full {cfg['name']} layer steps ({cfg['tokens']} tokens each, whole-tensor "
+                      f"dequantize per access as the reference property does), torch CPU, {cpu_model}",
+            "seconds": round(dt, 2)}
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (got --gpus {args.gpus}, "
+              f"WORLD_SIZE={world}); the expert-parallel sharding design is described in DESIGN.md",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from llada_quant_amd.runtime import _lib
+    from llada_quant_amd.runtime.fused_moe import _check_weights, workspace_bytes
+
+    cfg = dict(experts=64, hidden=2048, inter=1024, top_k=8)
+    cfg.update(CONFIGS[args.config])
+    E, H, I, k, T = cfg["experts"], cfg["hidden"], cfg["inter"], cfg["top_k"], cfg["tokens"]
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+
+    vb = 0.5 if cfg["bits"] == 4 else 1.0
+    per_copy = E * 3 * I * H * vb * (1 + 8 / 128 / vb)
+    copies = args.copies or max(3, int(3 * 256e6 // per_copy) + 1)
+    layers, x, logits = build_workload(torch, cfg, copies, args.seed, dev)
+
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev)
+    ws_bytes = workspace_bytes(T, H, I, E, k)
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    ids = torch.empty(T, k, dtype=torch.int32, device=dev)
+    calls = []
+    for q1, q2 in layers:
+        g1, g2, _ = _check_weights(x, q1, q2)
+        calls.append((
+            _lib.ptr(x), _lib.ptr(logits), _lib.LQ_F32, T, H, I, E, k, int(cfg["renorm"]), _lib.ptr(q1.q),
+            _lib.ptr(q1.scale), _lib.ptr(q2.q), _lib.ptr(q2.scale), cfg["bits"], g1, g2, _lib.ptr(workspace),
+            ws_bytes, _lib.ptr(out), _lib.ptr(ids), ctypes.c_void_p(stream.cuda_stream),
+        ))
+
+    def step(i):
+        rc = lib.lq_moe_layer(*calls[i % len(calls)])
+        if rc:
+            _lib.check(rc, "moe_layer")
+
+    hip = Hip()
+    # layer-call kernel boundaries: 0 start, 1 route, 2 permute, 3 GEMM1, 4 GEMM2, 5 combine
+    n_marks = 6
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    n_active = int((torch.bincount(ids.reshape(-1).long(), minlength=E) > 0).sum())
+
+    marks = [[hip.event() if j in (2, 3) else None for j in range(n_marks)] for _ in range(args.steps)]
+    arrays = [(ctypes.c_void_p * n_marks)(*[m.value if m is not None else None for m in row]) for row in marks]
+    t_start, t_end = hip.event(), hip.event()
+    hip_stream = ctypes.c_void_p(stream.cuda_stream)
+    hip.lib.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+
+    torch.cuda.synchronize()  # barrier (one rank) + sync on both sides of the timed region
+    wall0 = time.perf_counter()
+    hip.lib.hipEventRecord(t_start, hip_stream)
+    for i in range(args.steps):
+        lib.lq_moe_profile_events(ctypes.cast(arrays[i], ctypes.c_void_p), n_marks)
+        step(i)
+    hip.lib.hipEventRecord(t_end, hip_stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    elapsed_ms = hip.elapsed_ms(t_start, t_end)
+    gemm1_ms = sum(hip.elapsed_ms(row[2], row[3]) for row in marks) / args.steps
+    for row in marks:
+        for m in row:
+            if m is not None:
+                hip.destroy(m)
+
+    ms_per_step = elapsed_ms / args.steps
+    value = T * args.steps / (elapsed_ms / 1e3)
+    layer_b, gemm1_b = layer_bytes(cfg, n_active)
+    if cfg["bound"] == "hbm":
+        achieved = gemm1_b / (gemm1_ms / 1e3) / 1e9
+        roofline = {"kernel": "moe_gemm GEMM1 (W1 gate+up, SwiGLU epilogue)", "bound": "hbm",
+                    "achieved": round(achieved, 1), "peak": MI355X_HBM_GBPS, "unit": "GB/s",
+                    "frac": round(achieved / MI355X_HBM_GBPS, 4), "traffic": None,
+                    "algorithmic_bytes": gemm1_b, "avg_ms": round(gemm1_ms, 5)}
+    else:
+        flops = 2.0 * T * k * 2 * I * H
+        achieved = flops / (gemm1_ms / 1e3) / 1e12
+        roofline = {"kernel": "moe_gemm GEMM1 (W1 gate+up, SwiGLU epilogue)", "bound": "mfma",
+                    "achieved": round(achieved, 1), "peak": MI355X_BF16_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(achieved / MI355X_BF16_TFLOPS, 4), "traffic": None,
+                    "algorithmic_flops": flops, "avg_ms": round(gemm1_ms, 5)}
+
+    result = {
+        "metric": "MoE-layer tokens/s W4A16 64E top-8 H2048; % HBM/MFMA roofline",
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{cfg['name']}: one MoE layer, {E} experts, hidden {H}, intermediate {I}, "
+                        f"INT{cfg['bits']} g128 {cfg['search']} scales, {T} tokens, top-{k}"
+                        + (", Zipf(1.1) router bias" if cfg["skew"] else ""),
+            "experts": E, "hidden": H, "intermediate": I, "top_k": k, "tokens": T, "bits": cfg["bits"],
+            "group_size": 128, "active_experts": n_active, "weight_copies": copies,
+            "layer_algorithmic_bytes": layer_b,
+            "layer_gbps": round(layer_b / (ms_per_step / 1e3) / 1e9, 1),
+            "wall_ms_per_step": round(wall / args.steps * 1e3, 5),
+        },
+        "roofline": roofline,
+    }
+    if not args.no_gpu_baseline:
+        result["gpu_dequant_then_gemm"] = gpu_dequant_then_gemm(torch, cfg, layers, x, logits,
+                                                                max(5, args.steps // 10), 3)
+    if not args.no_cpu:
+        base = cpu_baseline(torch, cfg, layers, x, logits, args.cpu_seconds)
+        # the two paths agree: one GPU step on weight copy 0 against the CPU reference output
+        step(0 if len(calls) > 0 else 0)
+        torch.cuda.synchronize()
+        sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+        from oracle import torch_ref
+        q1, q2 = layers[0]
+        ref, _ = torch_ref.packed_layer(*[t.cpu() for t in (x, logits.float(), q1.q, q1.scale, q2.q, q2.scale)],
+                                        cfg["bits"], 128, k, cfg["renorm"])
+        diff = (out.float().cpu() - ref.float()).abs()
+        base["gpu_vs_cpu_max_abs"] = float(diff.max())
+        base["gpu_vs_cpu_mean_rel"] = float(diff.sum() / ref.float().abs().sum())
+        result["cpu_baseline"] = base
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

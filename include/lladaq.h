@@ -182,6 +182,32 @@ int lq_moe_forward(const void *x, int64_t T, int H, int I, int E, int k,
                    const float *topk_weights, void *workspace,
                    size_t ws_bytes, void *out, lq_stream_t stream);
 
+/*
+ * The whole MoE layer from router logits: lq_route_topk into the workspace,
+ * then lq_moe_forward (the TritonFusedMoEBlock.forward sequence after the
+ * gate: softmax -> topk -> fused_moe; trajectory/llada.py:228-234 and
+ * INFERENCE_REPO_CHANGES.md:110-111).  One host call, one stream.
+ *   logits [T, E] in logits_dtype; topk_ids_out (optional, [T, k] int32)
+ *   receives the routing; all other arguments as lq_moe_forward.
+ */
+int lq_moe_layer(const void *x, const void *logits, int logits_dtype,
+                 int64_t T, int H, int I, int E, int k, int renormalize,
+                 const int8_t *q1, const float *s1, const int8_t *q2,
+                 const float *s2, int bits, int64_t group_w1,
+                 int64_t group_w2, void *workspace, size_t ws_bytes,
+                 void *out, int32_t *topk_ids_out, lq_stream_t stream);
+
+/*
+ * Measurement hook (no counterpart in the reference; its timing is host-side,
+ * benchmarks/bench_generation_latency.py:51-72).  Registers caller-owned
+ * hipEvent_t handles that the NEXT lq_moe_forward / lq_moe_layer call on
+ * this thread records on its stream: events[0] before its first kernel and
+ * events[i] after its i-th kernel (layer: route, permute, GEMM1, GEMM2,
+ * combine; forward: permute, GEMM1, GEMM2, combine).  NULL entries are
+ * skipped; the registration is consumed by that one call.
+ */
+int lq_moe_profile_events(void *const *events, int n_events);
+
 #ifdef __cplusplus
 }
 #endif

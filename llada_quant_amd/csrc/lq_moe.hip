@@ -325,7 +325,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
 }
 
 struct WsLayout {
-  size_t counts, offsets, sorted, units, n_units, act, ybuf, total;
+  size_t counts, offsets, sorted, units, n_units, ids, weights, act, ybuf, total;
 };
 
 inline size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
@@ -344,48 +344,56 @@ WsLayout ws_layout(int64_t T, int H, int I, int E, int k) {
   const int mc = unit_rows_for(N, E);
   WsLayout w;
   size_t off = 0;
-  w.counts = off;
-  off = align256(off + sizeof(int32_t) * E);
-  w.offsets = off;
-  off = align256(off + sizeof(int32_t) * (E + 1));
-  w.sorted = off;
-  off = align256(off + sizeof(int32_t) * N);
-  w.units = off;
-  off = align256(off + sizeof(int32_t) * 3 * max_units_for(N, E, mc));
-  w.n_units = off;
-  off = align256(off + sizeof(int32_t));
-  w.act = off;
-  off = align256(off + sizeof(uint16_t) * N * I);
-  w.ybuf = off;
-  off = align256(off + sizeof(float) * N * H);
+  auto take = [&](size_t &field, size_t bytes) {
+    field = off;
+    off = align256(off + bytes);
+  };
+  take(w.counts, sizeof(int32_t) * E);
+  take(w.offsets, sizeof(int32_t) * (E + 1));
+  take(w.sorted, sizeof(int32_t) * N);
+  take(w.units, sizeof(int32_t) * 3 * max_units_for(N, E, mc));
+  take(w.n_units, sizeof(int32_t));
+  take(w.ids, sizeof(int32_t) * N);
+  take(w.weights, sizeof(float) * N);
+  take(w.act, sizeof(uint16_t) * N * I);
+  take(w.ybuf, sizeof(float) * N * H);
   w.total = off;
   return w;
 }
 
 template <int BITS, int NRT>
-void launch_gemms(const MoeArgs &a, int64_t max_units, hipStream_t st) {
-  const int64_t g1 = max_units * (a.I >> 6);
-  const int64_t g2 = max_units * (a.H >> 7);
-  moe_gemm_kernel<BITS, NRT, true><<<static_cast<int>(g1), kThreads, 0, st>>>(a);
-  moe_gemm_kernel<BITS, NRT, false><<<static_cast<int>(g2), kThreads, 0, st>>>(a);
+void launch_gemm1(const MoeArgs &a, int64_t max_units, hipStream_t st) {
+  moe_gemm_kernel<BITS, NRT, true><<<static_cast<int>(max_units * (a.I >> 6)), kThreads, 0, st>>>(a);
+}
+template <int BITS, int NRT>
+void launch_gemm2(const MoeArgs &a, int64_t max_units, hipStream_t st) {
+  moe_gemm_kernel<BITS, NRT, false><<<static_cast<int>(max_units * (a.H >> 7)), kThreads, 0, st>>>(a);
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-}  // namespace
-}  // namespace lq
+// Measurement hook (lq_moe_profile_events): caller-owned hipEvent_t handles
+// recorded on the call's stream at the kernel boundaries of the next layer
+// call on this thread.
+thread_local void *const *t_prof_events = nullptr;
+thread_local int t_prof_n = 0;
 
-using namespace lq;
+struct ProfileMarks {
+  void *const *ev;
+  int n;
+  hipStream_t st;
+  int rc = LQ_OK;
+  void mark(int i) {
+    if (ev && i < n && ev[i] && rc == LQ_OK) {
+      hipError_t e = hipEventRecord(static_cast<hipEvent_t>(ev[i]), st);
+      if (e != hipSuccess) rc = fail(LQ_ERR_RUNTIME, std::string("hipEventRecord failed: ") + hipGetErrorString(e));
+    }
+  }
+};
 
-extern "C" size_t lq_moe_workspace_bytes(int64_t T, int H, int I, int E, int k) {
-  if (T < 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
-  return ws_layout(T, H, I, E, k).total;
-}
-
-extern "C" int lq_moe_forward(const void *x, int64_t T, int H, int I, int E, int k, const int8_t *q1,
-                              const float *s1, const int8_t *q2, const float *s2, int bits, int64_t group_w1,
-                              int64_t group_w2, const int32_t *topk_ids, const float *topk_weights,
-                              void *workspace, size_t ws_bytes, void *out, lq_stream_t stream) {
+int validate_layer(const void *x, int64_t T, int H, int I, int E, int k, const int8_t *q1, const float *s1,
+                   const int8_t *q2, const float *s2, int bits, int64_t group_w1, int64_t group_w2,
+                   void *workspace, size_t ws_bytes, void *out) {
   if (bits != 4 && bits != 8) return fail(LQ_ERR_VALUE, "bits must be 8 or 4, got " + std::to_string(bits));
   if (T < 0 || H <= 0 || I <= 0 || k <= 0) return fail(LQ_ERR_VALUE, "moe_forward: bad shape");
   if (E < 1 || E > kMaxExperts)
@@ -402,18 +410,27 @@ extern "C" int lq_moe_forward(const void *x, int64_t T, int H, int I, int E, int
   const int64_t N = T * k;
   if (N > 0x7FFFFFFF / (H > I ? H : I)) return fail(LQ_ERR_UNSUPPORTED, "moe_forward: too many tokens");
   if (T == 0) return LQ_OK;
-  if (!x || !q1 || !s1 || !q2 || !s2 || !topk_ids || !topk_weights || !workspace || !out)
-    return fail(LQ_ERR_VALUE, "moe_forward: null pointer");
+  if (!x || !q1 || !s1 || !q2 || !s2 || !workspace || !out) return fail(LQ_ERR_VALUE, "moe_forward: null pointer");
   if (!aligned16(x) || !aligned16(q1) || !aligned16(q2) || !aligned16(workspace) || !aligned16(out))
     return fail(LQ_ERR_VALUE, "moe_forward: x, q1, q2, workspace and out must be 16-byte aligned");
-  const WsLayout w = ws_layout(T, H, I, E, k);
-  if (ws_bytes < w.total)
+  const size_t need = ws_layout(T, H, I, E, k).total;
+  if (ws_bytes < need)
     return fail(LQ_ERR_VALUE, "moe_forward: workspace too small (" + std::to_string(ws_bytes) + " < " +
-                                  std::to_string(w.total) + ")");
-  char *ws = static_cast<char *>(workspace);
+                                  std::to_string(need) + ")");
+  return LQ_OK;
+}
+
+// permute -> GEMM1 -> GEMM2 -> combine, marks[first_mark ..] at each boundary
+int moe_forward_impl(const void *x, int64_t T, int H, int I, int E, int k, const int8_t *q1, const float *s1,
+                     const int8_t *q2, const float *s2, int bits, int64_t group_w1, int64_t group_w2,
+                     const int32_t *topk_ids, const float *topk_weights, char *ws, void *out, hipStream_t st,
+                     ProfileMarks &pm, int first_mark) {
+  const WsLayout w = ws_layout(T, H, I, E, k);
+  const int64_t N = T * k;
   const int mc = unit_rows_for(N, E);
   const int64_t max_units = max_units_for(N, E, mc);
-  const hipStream_t st = as_stream(stream);
+  const int64_t g1 = effective_group(H, group_w1);
+  const int64_t g2 = effective_group(I, group_w2);
 
   MoeArgs a;
   a.x = static_cast<const uint16_t *>(x);
@@ -444,18 +461,88 @@ extern "C" int lq_moe_forward(const void *x, int64_t T, int H, int I, int E, int
                           mc, reinterpret_cast<int32_t *>(ws + w.units), reinterpret_cast<int32_t *>(ws + w.n_units),
                           st);
   if (rc) return rc;
-  if (bits == 4) {
-    if (mc == 16) launch_gemms<4, 1>(a, max_units, st);
-    else if (mc == 32) launch_gemms<4, 2>(a, max_units, st);
-    else launch_gemms<4, 4>(a, max_units, st);
-  } else {
-    if (mc == 16) launch_gemms<8, 1>(a, max_units, st);
-    else if (mc == 32) launch_gemms<8, 2>(a, max_units, st);
-    else launch_gemms<8, 4>(a, max_units, st);
+  pm.mark(first_mark);
+#define LQ_GEMM(WHICH)                                       \
+  if (bits == 4) {                                           \
+    if (mc == 16) WHICH<4, 1>(a, max_units, st);             \
+    else if (mc == 32) WHICH<4, 2>(a, max_units, st);        \
+    else WHICH<4, 4>(a, max_units, st);                      \
+  } else {                                                   \
+    if (mc == 16) WHICH<8, 1>(a, max_units, st);             \
+    else if (mc == 32) WHICH<8, 2>(a, max_units, st);        \
+    else WHICH<8, 4>(a, max_units, st);                      \
   }
+  LQ_GEMM(launch_gemm1);
+  pm.mark(first_mark + 1);
+  LQ_GEMM(launch_gemm2);
+#undef LQ_GEMM
   rc = check_launch("moe_gemm");
   if (rc) return rc;
+  pm.mark(first_mark + 2);
   const int64_t nthreads = T * (H >> 2);
   combine_kernel<<<static_cast<int>(ceil_div(nthreads, 256)), 256, 0, st>>>(a.ybuf, topk_ids, T, H, k, E, a.out);
-  return check_launch("moe_combine");
+  rc = check_launch("moe_combine");
+  if (rc) return rc;
+  pm.mark(first_mark + 3);
+  return pm.rc;
+}
+
+ProfileMarks take_profile(hipStream_t st) {
+  ProfileMarks pm{t_prof_events, t_prof_n, st};
+  t_prof_events = nullptr;
+  t_prof_n = 0;
+  return pm;
+}
+
+}  // namespace
+
+}  // namespace lq
+
+using namespace lq;
+
+extern "C" size_t lq_moe_workspace_bytes(int64_t T, int H, int I, int E, int k) {
+  if (T < 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
+  return ws_layout(T, H, I, E, k).total;
+}
+
+extern "C" int lq_moe_profile_events(void *const *events, int n_events) {
+  if (n_events < 0) return fail(LQ_ERR_VALUE, "moe_profile_events: negative count");
+  t_prof_events = n_events ? events : nullptr;
+  t_prof_n = n_events;
+  return LQ_OK;
+}
+
+extern "C" int lq_moe_forward(const void *x, int64_t T, int H, int I, int E, int k, const int8_t *q1,
+                              const float *s1, const int8_t *q2, const float *s2, int bits, int64_t group_w1,
+                              int64_t group_w2, const int32_t *topk_ids, const float *topk_weights,
+                              void *workspace, size_t ws_bytes, void *out, lq_stream_t stream) {
+  const hipStream_t st = as_stream(stream);
+  ProfileMarks pm = take_profile(st);
+  int rc = validate_layer(x, T, H, I, E, k, q1, s1, q2, s2, bits, group_w1, group_w2, workspace, ws_bytes, out);
+  if (rc || T == 0) return rc;
+  if (!topk_ids || !topk_weights) return fail(LQ_ERR_VALUE, "moe_forward: null routing pointer");
+  pm.mark(0);
+  return moe_forward_impl(x, T, H, I, E, k, q1, s1, q2, s2, bits, group_w1, group_w2, topk_ids, topk_weights,
+                          static_cast<char *>(workspace), out, st, pm, 1);
+}
+
+extern "C" int lq_moe_layer(const void *x, const void *logits, int logits_dtype, int64_t T, int H, int I, int E,
+                            int k, int renormalize, const int8_t *q1, const float *s1, const int8_t *q2,
+                            const float *s2, int bits, int64_t group_w1, int64_t group_w2, void *workspace,
+                            size_t ws_bytes, void *out, int32_t *topk_ids_out, lq_stream_t stream) {
+  const hipStream_t st = as_stream(stream);
+  ProfileMarks pm = take_profile(st);
+  int rc = validate_layer(x, T, H, I, E, k, q1, s1, q2, s2, bits, group_w1, group_w2, workspace, ws_bytes, out);
+  if (rc || T == 0) return rc;
+  if (!logits) return fail(LQ_ERR_VALUE, "moe_layer: null logits");
+  char *ws = static_cast<char *>(workspace);
+  const WsLayout w = ws_layout(T, H, I, E, k);
+  int32_t *ids = topk_ids_out ? topk_ids_out : reinterpret_cast<int32_t *>(ws + w.ids);
+  float *weights = reinterpret_cast<float *>(ws + w.weights);
+  pm.mark(0);
+  rc = launch_route_topk(logits, logits_dtype, T, E, k, renormalize, ids, weights, st);
+  if (rc) return rc;
+  pm.mark(1);
+  return moe_forward_impl(x, T, H, I, E, k, q1, s1, q2, s2, bits, group_w1, group_w2, ids, weights, ws, out, st,
+                          pm, 2);
 }

@@ -13,4 +13,8 @@ constexpr int kMaxExperts = 256;
 int launch_permute(const int32_t *ids, int64_t N, int E, int32_t *counts, int32_t *offsets, int32_t *sorted,
                    int unit_rows, int32_t *units, int32_t *n_units, hipStream_t st);
 
+// Top-k softmax router launch (validates its arguments).
+int launch_route_topk(const void *logits, int logits_dtype, int64_t T, int E, int k, int renormalize,
+                      int32_t *topk_ids, float *topk_weights, hipStream_t st);
+
 }  // namespace lq

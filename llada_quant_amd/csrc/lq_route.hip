@@ -244,8 +244,9 @@ int launch_permute(const int32_t *ids, int64_t N, int E, int32_t *counts, int32_
 
 using namespace lq;
 
-extern "C" int lq_route_topk(const void *logits, int logits_dtype, int64_t T, int E, int k, int renormalize,
-                             int32_t *topk_ids, float *topk_weights, lq_stream_t stream) {
+namespace lq {
+int launch_route_topk(const void *logits, int logits_dtype, int64_t T, int E, int k, int renormalize,
+                      int32_t *topk_ids, float *topk_weights, hipStream_t st) {
   if (logits_dtype != LQ_F32 && logits_dtype != LQ_BF16 && logits_dtype != LQ_F16)
     return fail(LQ_ERR_VALUE, "route_topk: logits must be float32, float16 or bfloat16");
   if (E < 1 || E > kMaxExperts)
@@ -256,7 +257,6 @@ extern "C" int lq_route_topk(const void *logits, int logits_dtype, int64_t T, in
   if (!logits || !topk_ids || !topk_weights) return fail(LQ_ERR_VALUE, "route_topk: null pointer");
   const int64_t blocks = ceil_div(T * 64, kRouteBlock);
   if (blocks > 0x7FFFFFFF) return fail(LQ_ERR_UNSUPPORTED, "route_topk: too many tokens");
-  const hipStream_t st = as_stream(stream);
 #define LQ_ROUTE_LAUNCH(EPL)                                                                         \
   LQ_DISPATCH_DTYPE(logits_dtype, LDT, {                                                             \
     route_topk_kernel<LDT, EPL><<<static_cast<int>(blocks), kRouteBlock, 0, st>>>(                   \
@@ -271,6 +271,12 @@ extern "C" int lq_route_topk(const void *logits, int logits_dtype, int64_t T, in
   }
 #undef LQ_ROUTE_LAUNCH
   return check_launch("route_topk");
+}
+}  // namespace lq
+
+extern "C" int lq_route_topk(const void *logits, int logits_dtype, int64_t T, int E, int k, int renormalize,
+                             int32_t *topk_ids, float *topk_weights, lq_stream_t stream) {
+  return launch_route_topk(logits, logits_dtype, T, E, k, renormalize, topk_ids, topk_weights, as_stream(stream));
 }
 
 extern "C" int lq_gather_topk_weights(const float *probs, const void *ids, int ids_int64, int64_t T, int E, int k,

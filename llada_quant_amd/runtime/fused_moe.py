@@ -26,7 +26,7 @@ import torch
 from ..algorithms.symmetric import QuantResult
 from . import _lib
 from .moe import PackedExpertTensor
-from .routing import gather_topk_weights, route_topk
+from .routing import gather_topk_weights
 
 PackedWeight = Union[PackedExpertTensor, QuantResult]
 
@@ -56,6 +56,39 @@ def fused_moe_packed(
     workspace: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """The layer on explicit operands: ``x [T, H]`` bf16, int32 ids and fp32 weights ``[T, k]``."""
+    g1, g2, I = _check_weights(x, w1, w2)
+    T, H = x.shape
+    E = w1.logical_shape[0]
+    k = topk_ids.shape[1]
+    if topk_ids.shape[0] != T or topk_weights.shape != topk_ids.shape:
+        raise ValueError("topk_ids / topk_weights must be [tokens, top_k]")
+    xc = x.contiguous()
+    ids = topk_ids.to(torch.int32).contiguous()
+    wts = topk_weights.to(torch.float32).contiguous()
+    q1, s1, q2, s2 = (t.contiguous() for t in (w1.q, w1.scale, w2.q, w2.scale))
+    device = _lib.require_hip(xc, ids, wts, q1, s1, q2, s2)
+    if out is None:
+        out = torch.empty(T, H, dtype=torch.bfloat16, device=device)
+    ws_need = workspace_bytes(T, H, I, E, k)
+    if workspace is None or workspace.numel() < ws_need:
+        workspace = torch.empty(max(ws_need, 1), dtype=torch.uint8, device=device)
+    if T:
+        lib = _lib.load()
+        with torch.cuda.device(device):
+            rc = lib.lq_moe_forward(
+                _lib.ptr(xc), T, H, I, E, k, _lib.ptr(q1), _lib.ptr(s1), _lib.ptr(q2), _lib.ptr(s2), w1.bits, g1, g2,
+                _lib.ptr(ids), _lib.ptr(wts), _lib.ptr(workspace), workspace.numel(), _lib.ptr(out),
+                _lib.stream(device),
+            )
+        _lib.check(rc, "fused_moe")
+    return out
+
+
+def _check_weights(x: torch.Tensor, w1: QuantResult, w2: QuantResult):
+    """Validate x and the packed operands on the host; returns (G1, G2, I).
+
+    Every operand shape is checked here because the kernels trust them.
+    """
     if x.dim() != 2:
         raise ValueError(f"x must be [tokens, hidden], got {tuple(x.shape)}")
     if x.dtype != torch.bfloat16:
@@ -88,29 +121,7 @@ def fused_moe_packed(
             raise ValueError(f"{what} have shape {got}, expected {want}")
     if w1.q.dtype != torch.int8 or w2.q.dtype != torch.int8:
         raise ValueError("packed expert codes must be int8")
-    k = topk_ids.shape[1]
-    if topk_ids.shape[0] != T or topk_weights.shape != topk_ids.shape:
-        raise ValueError("topk_ids / topk_weights must be [tokens, top_k]")
-    xc = x.contiguous()
-    ids = topk_ids.to(torch.int32).contiguous()
-    wts = topk_weights.to(torch.float32).contiguous()
-    q1, s1, q2, s2 = (t.contiguous() for t in (w1.q, w1.scale, w2.q, w2.scale))
-    device = _lib.require_hip(xc, ids, wts, q1, s1, q2, s2)
-    if out is None:
-        out = torch.empty(T, H, dtype=torch.bfloat16, device=device)
-    ws_need = workspace_bytes(T, H, I, E, k)
-    if workspace is None or workspace.numel() < ws_need:
-        workspace = torch.empty(max(ws_need, 1), dtype=torch.uint8, device=device)
-    if T:
-        lib = _lib.load()
-        with torch.cuda.device(device):
-            rc = lib.lq_moe_forward(
-                _lib.ptr(xc), T, H, I, E, k, _lib.ptr(q1), _lib.ptr(s1), _lib.ptr(q2), _lib.ptr(s2), w1.bits, g1, g2,
-                _lib.ptr(ids), _lib.ptr(wts), _lib.ptr(workspace), workspace.numel(), _lib.ptr(out),
-                _lib.stream(device),
-            )
-        _lib.check(rc, "fused_moe")
-    return out
+    return g1, g2, I
 
 
 def fused_moe(
@@ -155,9 +166,41 @@ def moe_layer(
     top_k: int,
     renormalize: bool = False,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Router + quantized experts: returns ``(output [..., H], topk_ids [T, k])``."""
-    ids, weights = route_topk(router_logits, top_k, renormalize)
+    """Router + quantized experts in one library call: ``(output [..., H], topk_ids [T, k] int32)``.
+
+    ``router_logits [..., E]`` are the gate's outputs; routing is
+    softmax(fp32) -> top-k (descending probability, ties to the lower id),
+    weights renormalized over the k experts when ``renormalize``.
+    """
+    q1 = _unpack_weight(w1, "w1")
+    q2 = _unpack_weight(w2, "w2")
     H = hidden_states.shape[-1]
-    out = fused_moe_packed(hidden_states.reshape(-1, H), _unpack_weight(w1, "w1"), _unpack_weight(w2, "w2"),
-                           ids, weights)
+    x = hidden_states.reshape(-1, H)
+    T = x.shape[0]
+    E = q1.logical_shape[0]
+    logits = router_logits.reshape(T, -1)
+    if logits.shape[1] != E:
+        raise ValueError(f"router_logits have {logits.shape[1]} experts, the weights {E}")
+    if not 1 <= top_k <= E:
+        raise ValueError(f"top_k must lie in [1, {E}], got {top_k}")
+    if logits.dtype not in _lib.DTYPE_CODES:
+        logits = logits.to(torch.float32)
+    logits = logits.contiguous()
+    # shape/dtype validation of the weights, shared with fused_moe_packed
+    g1, g2, I = _check_weights(x, q1, q2)
+    xc = x.contiguous()
+    q1c, s1, q2c, s2 = (t.contiguous() for t in (q1.q, q1.scale, q2.q, q2.scale))
+    device = _lib.require_hip(xc, logits, q1c, s1, q2c, s2)
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=device)
+    ids = torch.empty(T, top_k, dtype=torch.int32, device=device)
+    workspace = torch.empty(max(workspace_bytes(T, H, I, E, top_k), 1), dtype=torch.uint8, device=device)
+    if T:
+        lib = _lib.load()
+        with torch.cuda.device(device):
+            rc = lib.lq_moe_layer(
+                _lib.ptr(xc), _lib.ptr(logits), _lib.dtype_code(logits.dtype, "router_logits"), T, H, I, E, top_k,
+                int(renormalize), _lib.ptr(q1c), _lib.ptr(s1), _lib.ptr(q2c), _lib.ptr(s2), q1.bits, g1, g2,
+                _lib.ptr(workspace), workspace.numel(), _lib.ptr(out), _lib.ptr(ids), _lib.stream(device),
+            )
+        _lib.check(rc, "moe_layer")
     return out.reshape(hidden_states.shape), ids
