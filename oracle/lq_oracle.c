@@ -128,7 +128,7 @@ int64_t oq_effective_group(int64_t k, int64_t group_size) {
 /* The search loss `work.pow_(2).sum(dim=-1)` (symmetric.py:198) is summed */
 /* this way; the order decides which candidate wins a near tie.  Checked   */
 /* bit-exact against torch for row lengths 1..8192 in                      */
-/* tests/test_oracle_sum_order.py.                                         */
+/* tests/test_oracle.py.                                                   */
 /* ---------------------------------------------------------------------- */
 
 #define OQ_LANES 8
@@ -146,7 +146,7 @@ static int64_t ceil_log2_i64(int64_t x) {
 /* multi_row_sum over `size` rows; row i supplies OQ_ILP accumulator inputs,
  * each of width `w` floats (w = OQ_LANES for vectors, 1 for scalars).
  * elem(i, k, l) = x[(i*OQ_ILP + k) * w + l]. */
-static void multi_row_sum(const float *x, int64_t size, int w, float *out /* [OQ_ILP][w] */) {
+static void multi_row_sum(const float *x, int64_t size, int w, float *out /* [OQ_ILP][OQ_LANES] */) {
   float acc[OQ_LEVELS][OQ_ILP][OQ_LANES];
   memset(acc, 0, sizeof(acc));
   int64_t level_power = ceil_log2_i64(size) / OQ_LEVELS;
@@ -175,7 +175,7 @@ static void multi_row_sum(const float *x, int64_t size, int w, float *out /* [OQ
     for (int k = 0; k < OQ_ILP; ++k)
       for (int l = 0; l < w; ++l) acc[0][k][l] += acc[j][k][l];
   for (int k = 0; k < OQ_ILP; ++k)
-    for (int l = 0; l < w; ++l) out[k * w + l] = acc[0][k][l];
+    for (int l = 0; l < w; ++l) out[k * OQ_LANES + l] = acc[0][k][l];
 }
 
 /* row_sum over `size` units of width w (units are vectors or scalars). */

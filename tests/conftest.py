@@ -30,6 +30,7 @@ VOCAB = 32
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a ROCm GPU (MI355X / gfx950) and liblladaq.so")
+    config.addinivalue_line("markers", "slow: CPU check over a full configuration-sized tensor (tens of seconds)")
 
 
 class FusedExpertBlock(nn.Module):
