@@ -4,9 +4,10 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c4|c3|c2|c1]
 
 A *step* is one quantized MoE layer over one batch: router (softmax top-k
-from logits), stable expert permutation, GEMM1 + SwiGLU, GEMM2 + routed
-weight, top-k combine -- one ``lq_moe_layer`` call (five kernels on one
-stream).  Inputs are resident in HBM before the timed region; weights rotate
+from logits, which also writes the K-slot permuted x), stable expert
+permutation and work list, persistent GEMM1 + SwiGLU, persistent GEMM2 +
+routed weight, top-k combine -- one ``lq_moe_layer`` call (five kernels on
+one stream).  Inputs are resident in HBM before the timed region; weights rotate
 over several independently quantized copies so every step streams its
 weights from HBM rather than from the 256 MB MALL.
 
@@ -15,9 +16,11 @@ hidden 2048, intermediate 1024, INT4 group 128 with MSE scales (grid 16),
 64 tokens ~N(0,1), top-8 routing with Zipf(1.1)-skewed router logits.
 
 One JSON line is printed.  Besides the contract fields it carries
-``roofline`` for the dominant kernel (GEMM1: HBM-bound at C4/C2, MFMA-bound
-at C3), timed with HIP events recorded by the library on the kernel's own
-stream inside the timed region, ``cpu_baseline`` (the reference's
+``roofline`` for the dominant kernel (GEMM1, the persistent W1 kernel with
+the SwiGLU epilogue: HBM-bound at C4/C2, MFMA-bound at C3), timed with HIP
+events recorded by the library on the kernel's own stream inside the timed
+region, per-stage times, the other weight form's timing
+(``folded_scales`` or ``exact_weights``), ``cpu_baseline`` (the reference's
 dequantize-then-matmul path on the host CPU, torch, bounded sample) and
 ``gpu_dequant_then_gemm`` (the same layer as dequantize-to-BF16 with the HIP
 dequant kernel, then torch BF16 batched GEMMs on the same GPU).
@@ -55,6 +58,8 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-gpu-baseline", action="store_true", help="skip the dequantize-then-GEMM leg")
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--folded", action="store_true",
+                   help="time the LQ_MOE_FOLDED_SCALES form (integer codes, fp32 group scale) as the headline")
     return p.parse_args()
 
 
@@ -116,14 +121,21 @@ def build_workload(torch, cfg, copies, seed, dev):
 
 
 def layer_bytes(cfg, n_active):
-    """Algorithmic HBM bytes of one layer and of its GEMM1 (compulsory traffic, read once)."""
+    """Algorithmic HBM bytes (compulsory traffic, each byte once) of the layer and of its two GEMM kernels.
+
+    GEMM1: packed w1 + its fp32 scales of every active expert, plus x [T, H]
+    bf16.  GEMM2: packed w2 + scales, plus the routing weights [T, k] fp32.
+    Layer: both, plus out [T, H] bf16, the router logits [T, E] fp32 and the
+    ids [T, k] int32.  Intermediates (act, slot outputs) are excluded.
+    """
     E, H, I, k, T = cfg["experts"], cfg["hidden"], cfg["inter"], cfg["top_k"], cfg["tokens"]
     vb = 0.5 if cfg["bits"] == 4 else 1.0
     w1 = 2 * I * H * vb + 2 * I * (H // 128) * 4
     w2 = H * I * vb + H * (I // 128) * 4
-    gemm1 = n_active * w1 + T * H * 2
-    layer = n_active * (w1 + w2) + T * H * 2 + T * H * 2 + T * E * 4 + T * k * 8
-    return int(layer), int(gemm1)
+    g1 = n_active * w1 + T * H * 2
+    g2 = n_active * w2 + T * k * 4
+    layer = g1 + g2 + T * H * 2 + T * E * 4 + T * k * 4
+    return int(layer), int(g1), int(g2)
 
 
 def gpu_dequant_then_gemm(torch, cfg, layers, x, logits, steps, warmup):
@@ -233,66 +245,77 @@ def main():
     workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
     ids = torch.empty(T, k, dtype=torch.int32, device=dev)
-    calls = []
-    for q1, q2 in layers:
-        g1, g2, _ = _check_weights(x, q1, q2)
-        calls.append((
-            _lib.ptr(x), _lib.ptr(logits), _lib.LQ_F32, T, H, I, E, k, int(cfg["renorm"]), _lib.ptr(q1.q),
-            _lib.ptr(q1.scale), _lib.ptr(q2.q), _lib.ptr(q2.scale), cfg["bits"], g1, g2, _lib.ptr(workspace),
-            ws_bytes, _lib.ptr(out), _lib.ptr(ids), ctypes.c_void_p(stream.cuda_stream),
-        ))
 
-    def step(i):
-        rc = lib.lq_moe_layer(*calls[i % len(calls)])
-        if rc:
-            _lib.check(rc, "moe_layer")
+    def make_calls(flags):
+        calls = []
+        for q1, q2 in layers:
+            g1, g2, _ = _check_weights(x, q1, q2)
+            calls.append((
+                _lib.ptr(x), _lib.ptr(logits), _lib.LQ_F32, T, H, I, E, k, int(cfg["renorm"]), _lib.ptr(q1.q),
+                _lib.ptr(q1.scale), _lib.ptr(q2.q), _lib.ptr(q2.scale), cfg["bits"], g1, g2, flags,
+                _lib.ptr(workspace), ws_bytes, _lib.ptr(out), _lib.ptr(ids), ctypes.c_void_p(stream.cuda_stream),
+            ))
+        return calls
 
     hip = Hip()
-    # layer-call kernel boundaries: 0 start, 1 route, 2 permute, 3 GEMM1, 4 GEMM2, 5 combine
-    n_marks = 6
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-    n_active = int((torch.bincount(ids.reshape(-1).long(), minlength=E) > 0).sum())
-
-    marks = [[hip.event() if j in (2, 3) else None for j in range(n_marks)] for _ in range(args.steps)]
-    arrays = [(ctypes.c_void_p * n_marks)(*[m.value if m is not None else None for m in row]) for row in marks]
-    t_start, t_end = hip.event(), hip.event()
-    hip_stream = ctypes.c_void_p(stream.cuda_stream)
     hip.lib.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    hip_stream = ctypes.c_void_p(stream.cuda_stream)
+    # stage boundaries of one lq_moe_layer call: 0 start, 1 route (+ x permute), 2 plan,
+    # 3 GEMM1 (+SwiGLU), 4 GEMM2 (+routed weight), 5 combine
+    n_marks = 6
 
-    torch.cuda.synchronize()  # barrier (one rank) + sync on both sides of the timed region
-    wall0 = time.perf_counter()
-    hip.lib.hipEventRecord(t_start, hip_stream)
-    for i in range(args.steps):
-        lib.lq_moe_profile_events(ctypes.cast(arrays[i], ctypes.c_void_p), n_marks)
-        step(i)
-    hip.lib.hipEventRecord(t_end, hip_stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    elapsed_ms = hip.elapsed_ms(t_start, t_end)
-    gemm1_ms = sum(hip.elapsed_ms(row[2], row[3]) for row in marks) / args.steps
-    for row in marks:
-        for m in row:
-            if m is not None:
+    def timed(calls, steps, warmup):
+        """(ms per step, mean ms per stage [route, plan, gemm1, gemm2, combine]) over `steps` steps."""
+        for i in range(warmup):
+            rc = lib.lq_moe_layer(*calls[i % len(calls)])
+            if rc:
+                _lib.check(rc, "moe_layer")
+        torch.cuda.synchronize()
+        marks = [[hip.event() for _ in range(n_marks)] for _ in range(steps)]
+        arrays = [(ctypes.c_void_p * n_marks)(*[m.value for m in row]) for row in marks]
+        t_start, t_end = hip.event(), hip.event()
+        torch.cuda.synchronize()  # barrier (one rank) + sync on both sides of the timed region
+        hip.lib.hipEventRecord(t_start, hip_stream)
+        for i in range(steps):
+            lib.lq_moe_profile_events(ctypes.cast(arrays[i], ctypes.c_void_p), n_marks)
+            rc = lib.lq_moe_layer(*calls[i % len(calls)])
+            if rc:
+                _lib.check(rc, "moe_layer")
+        hip.lib.hipEventRecord(t_end, hip_stream)
+        torch.cuda.synchronize()
+        total_ms = hip.elapsed_ms(t_start, t_end)
+        stage_ms = [sum(hip.elapsed_ms(row[j], row[j + 1]) for row in marks) / steps for j in range(n_marks - 1)]
+        for row in marks:
+            for m in row:
                 hip.destroy(m)
+        hip.destroy(t_start)
+        hip.destroy(t_end)
+        return total_ms / steps, stage_ms
 
-    ms_per_step = elapsed_ms / args.steps
-    value = T * args.steps / (elapsed_ms / 1e3)
-    layer_b, gemm1_b = layer_bytes(cfg, n_active)
+    calls = make_calls(_lib.LQ_MOE_FOLDED_SCALES if args.folded else 0)
+    wall0 = time.perf_counter()
+    ms_per_step, stage_ms = timed(calls, args.steps, args.warmup)
+    wall = time.perf_counter() - wall0
+    value = T / (ms_per_step / 1e3)
+    n_active = int((torch.bincount(ids.reshape(-1).long(), minlength=E) > 0).sum())
+    layer_b, g1_b, g2_b = layer_bytes(cfg, n_active)
+    gemm1_ms = stage_ms[2]
+    kname = "moe_gemm_kernel<G1> (W1 gate+up, SwiGLU epilogue; persistent)"
     if cfg["bound"] == "hbm":
-        achieved = gemm1_b / (gemm1_ms / 1e3) / 1e9
-        roofline = {"kernel": "moe_gemm GEMM1 (W1 gate+up, SwiGLU epilogue)", "bound": "hbm",
-                    "achieved": round(achieved, 1), "peak": MI355X_HBM_GBPS, "unit": "GB/s",
-                    "frac": round(achieved / MI355X_HBM_GBPS, 4), "traffic": None,
-                    "algorithmic_bytes": gemm1_b, "avg_ms": round(gemm1_ms, 5)}
+        achieved = g1_b / (gemm1_ms / 1e3) / 1e9
+        roofline = {"kernel": kname, "bound": "hbm", "achieved": round(achieved, 1), "peak": MI355X_HBM_GBPS,
+                    "unit": "GB/s", "frac": round(achieved / MI355X_HBM_GBPS, 4), "traffic": None,
+                    "algorithmic_bytes": g1_b, "avg_ms": round(gemm1_ms, 5)}
     else:
         flops = 2.0 * T * k * 2 * I * H
         achieved = flops / (gemm1_ms / 1e3) / 1e12
-        roofline = {"kernel": "moe_gemm GEMM1 (W1 gate+up, SwiGLU epilogue)", "bound": "mfma",
-                    "achieved": round(achieved, 1), "peak": MI355X_BF16_TFLOPS, "unit": "TFLOP/s",
-                    "frac": round(achieved / MI355X_BF16_TFLOPS, 4), "traffic": None,
+        roofline = {"kernel": kname, "bound": "mfma", "achieved": round(achieved, 1), "peak": MI355X_BF16_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(achieved / MI355X_BF16_TFLOPS, 4), "traffic": None,
                     "algorithmic_flops": flops, "avg_ms": round(gemm1_ms, 5)}
+    stages = {name: round(v, 5) for name, v in zip(("route", "plan", "gemm1", "gemm2", "combine"), stage_ms)}
+    stages["gemm2_gbps"] = round(g2_b / (stage_ms[3] / 1e3) / 1e9, 1)
+    other_ms, other_stage = timed(make_calls(0 if args.folded else _lib.LQ_MOE_FOLDED_SCALES),
+                                  max(10, args.steps // 4), 3)
 
     result = {
         "metric": "MoE-layer tokens/s W4A16 64E top-8 H2048; % HBM/MFMA roofline",
@@ -313,11 +336,16 @@ def main():
                         + (", Zipf(1.1) router bias" if cfg["skew"] else ""),
             "experts": E, "hidden": H, "intermediate": I, "top_k": k, "tokens": T, "bits": cfg["bits"],
             "group_size": 128, "active_experts": n_active, "weight_copies": copies,
+            "weights_in_mfma": "folded: exact codes, fp32 group scale" if args.folded else "exact bf16(fp32(q)*s)",
             "layer_algorithmic_bytes": layer_b,
             "layer_gbps": round(layer_b / (ms_per_step / 1e3) / 1e9, 1),
-            "wall_ms_per_step": round(wall / args.steps * 1e3, 5),
+            "wall_ms_per_step": round(wall / (args.steps + args.warmup) * 1e3, 5),
+            "stage_ms": stages,
         },
         "roofline": roofline,
+        ("exact_weights" if args.folded else "folded_scales"): {
+            "ms_per_step": round(other_ms, 5), "gemm1_ms": round(other_stage[2], 5),
+            "gemm2_ms": round(other_stage[3], 5), "value": round(T / (other_ms / 1e3), 1), "unit": "tokens/s"},
     }
     if not args.no_gpu_baseline:
         result["gpu_dequant_then_gemm"] = gpu_dequant_then_gemm(torch, cfg, layers, x, logits,
@@ -325,7 +353,7 @@ def main():
     if not args.no_cpu:
         base = cpu_baseline(torch, cfg, layers, x, logits, args.cpu_seconds)
         # the two paths agree: one GPU step on weight copy 0 against the CPU reference output
-        step(0 if len(calls) > 0 else 0)
+        _lib.check(lib.lq_moe_layer(*calls[0]), "moe_layer")
         torch.cuda.synchronize()
         sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
         from oracle import torch_ref

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define LQ_ABI_VERSION 1
+#define LQ_ABI_VERSION 2
 
 /* status codes */
 #define LQ_OK 0
@@ -41,6 +41,9 @@ extern "C" {
 #define LQ_F32 0
 #define LQ_F16 1
 #define LQ_BF16 2
+
+/* lq_moe_forward / lq_moe_layer flags */
+#define LQ_MOE_FOLDED_SCALES 1 /* exact integer codes in the MFMA, group scale in fp32 */
 
 /* scale search codes (QuantConfig.scale_search) */
 #define LQ_SCALE_AMAX 0
@@ -160,7 +163,7 @@ size_t lq_moe_workspace_bytes(int64_t T, int H, int I, int E, int k);
  * The quantized expert layer (fused_moe with packed weights):
  *   out[t] = sum_j w[t,j] * W2[e]^T act(W1[e] x[t]),  e = ids[t,j]
  *   act(g, u) = bf16(bf16(silu(bf16(g))) * bf16(u)), gate = W1[e][:I],
- *   up = W1[e][I:], weights dequantized in registers as bf16(fp32(q)*s).
+ *   up = W1[e][I:].
  * Replaces dequantize-then-fused_moe: runtime/moe.py:199-216 feeding
  * fused_moe(x, w1, w2, gating_output, topk_ids) (INFERENCE_REPO_CHANGES.md:
  * 37-63, 110-111, 259-265, 296-309).
@@ -169,16 +172,25 @@ size_t lq_moe_workspace_bytes(int64_t T, int H, int I, int E, int k);
  *   q2  [E, H, I]  int8 / [E, H, I/2]  packed, s2 [E, H, I/G2]  f32
  *   group_w1, group_w2: group lengths G1 (along H) and G2 (along I) as the
  *           quantizer recorded them for each tensor (-1 = one group per row)
+ *   flags   0: the matrix cores consume the reference's dequantized weights
+ *           bf16(fp32(q) * s) bit for bit (dequantize-then-matmul up to the
+ *           fp32 summation order).  LQ_MOE_FOLDED_SCALES: the codes enter as
+ *           exact small integers and each group's fp32 scale multiplies the
+ *           integer dot product of its 128-wide K chunk -- cheaper, but the
+ *           weights are not rounded to bf16 first, which moves the output by
+ *           about the reference tolerance (mean-relative ~5e-3); group lengths
+ *           that are not multiples of 128 ignore the flag.
  *   topk_ids [T, k] int32, topk_weights [T, k] f32; ids outside [0, E)
  *           contribute nothing
  *   workspace of ws_bytes >= lq_moe_workspace_bytes(T, H, I, E, k)
- * Requires H % 128 == 0, I % 64 == 0, and group lengths (after the per-row
- * fallback) that are multiples of 32.
+ * Requires H % 128 == 0, I % 64 == 0, group lengths (after the per-row
+ * fallback) that are multiples of 32, and T <= 262144.  Kernels on `stream`
+ * (x permute, plan, GEMM1, GEMM2, combine); no host synchronisation.
  */
 int lq_moe_forward(const void *x, int64_t T, int H, int I, int E, int k,
                    const int8_t *q1, const float *s1, const int8_t *q2,
                    const float *s2, int bits, int64_t group_w1,
-                   int64_t group_w2, const int32_t *topk_ids,
+                   int64_t group_w2, int flags, const int32_t *topk_ids,
                    const float *topk_weights, void *workspace,
                    size_t ws_bytes, void *out, lq_stream_t stream);
 
@@ -194,16 +206,17 @@ int lq_moe_layer(const void *x, const void *logits, int logits_dtype,
                  int64_t T, int H, int I, int E, int k, int renormalize,
                  const int8_t *q1, const float *s1, const int8_t *q2,
                  const float *s2, int bits, int64_t group_w1,
-                 int64_t group_w2, void *workspace, size_t ws_bytes,
-                 void *out, int32_t *topk_ids_out, lq_stream_t stream);
+                 int64_t group_w2, int flags, void *workspace,
+                 size_t ws_bytes, void *out, int32_t *topk_ids_out,
+                 lq_stream_t stream);
 
 /*
  * Measurement hook (no counterpart in the reference; its timing is host-side,
  * benchmarks/bench_generation_latency.py:51-72).  Registers caller-owned
  * hipEvent_t handles that the NEXT lq_moe_forward / lq_moe_layer call on
  * this thread records on its stream: events[0] before its first kernel and
- * events[i] after its i-th kernel (layer: route, permute, GEMM1, GEMM2,
- * combine; forward: permute, GEMM1, GEMM2, combine).  NULL entries are
+ * events[i] after the i-th stage (layer: route, plan, GEMM1, GEMM2, combine;
+ * forward: x permute + plan, GEMM1, GEMM2, combine).  NULL entries are
  * skipped; the registration is consumed by that one call.
  */
 int lq_moe_profile_events(void *const *events, int n_events);

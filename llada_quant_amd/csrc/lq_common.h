@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+#include <cstddef>
 #include <string>
 
 #include "../../include/lladaq.h"
@@ -118,6 +120,21 @@ __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
   return v;
+}
+
+// 8 consecutive bf16 (dwords = element pairs 01 23 45 67) -> the K-slot order
+// [0,4,1,5,2,6,3,7] of the MoE kernel's MFMA fragments (dwords 04 15 26 37)
+__device__ __forceinline__ uint4 permute_kslots(uint4 v) {
+  return make_uint4(__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
+                    __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u));
+}
+
+// storage column of K index f in a permuted row: slot order [0,4,1,5,2,6,3,7]
+// within each group of 8, i.e. element e of a group lands in slot 2e (e < 4)
+// or 2(e - 4) + 1
+__device__ __forceinline__ int kslot(int f) {
+  const int e = f & 7;
+  return (f & ~7) | (e < 4 ? 2 * e : 2 * (e - 4) + 1);
 }
 
 // dispatch a runtime dtype code to a template parameter

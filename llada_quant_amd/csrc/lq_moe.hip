@@ -1,31 +1,50 @@
-// lq_moe.hip -- the quantized MoE expert layer on gfx950: grouped W4A16 /
-// W8A16 GEMMs that read packed weights straight from HBM, dequantize them in
-// registers (bit-exact to the reference's bf16(fp32(q) * s)) and feed
-// v_mfma_f32_16x16x32_bf16, with the SwiGLU activation fused into GEMM1 and
-// the routed-weight scaling fused into GEMM2.
+// lq_moe.hip -- the quantized MoE expert layer on gfx950.
 //
 // Replaces dequantize_tensor (runtime/moe.py:199-216) feeding the external
-// fused_moe (INFERENCE_REPO_CHANGES.md:37-63, 259-265, 296-309).
+// fused_moe (INFERENCE_REPO_CHANGES.md:37-63, 259-265, 296-309): packed
+// INT4/INT8 expert weights are read straight from HBM, unpacked in registers
+// and fed to v_mfma_f32_16x16x32_bf16; no BF16 copy of a weight is written.
 //
-// Data flow of one forward (all on one stream, no host sync):
-//   permute   ids -> counts/offsets/sorted + work units (expert, rows)
-//   GEMM1     act[p, :]  = swiglu(x[t(p)] . W1[e]^T)          p = sorted pos
-//   GEMM2     y[a, :]    = w[a] * (act[p] . W2[e]^T)          a = assignment
-//   combine   out[t, :]  = bf16(sum_j y[t*k + j, :])
+// One forward is a few launches on one stream, with no host synchronisation:
 //
-// Work decomposition: a unit is up to 16*NRT consecutive sorted rows of one
-// expert.  A workgroup (4 waves) computes one unit against 8 column tiles of
-// 16 weight rows (GEMM1: 4 gate + 4 up tiles, 64 output features; GEMM2: 8
-// tiles, 128 output features), over the full reduction axis split across the
-// 4 waves; the 4 partials are summed through LDS in fixed order, so results
-// are deterministic.
+//   plan     (one workgroup) stable counting sort of the T*k assignments by
+//            expert, and the work list of the layer:
+//              G1 items  (expert, 64-feature slice, block of <= 32 rows)
+//              G2 items  (expert, 128-row output slice, block of <= 32 rows)
+//   G1       (persistent, items in ticket order)
+//              act[p, f] = swiglu(x[t(p)] . W1[e]^T)      p = sorted row
+//   G2       (persistent, items in ticket order)
+//              y[a, h]   = w[a] * (act[p] . W2[e]^T)      a = assignment
+//   combine  out[t, h] = bf16(sum_j y[t*k + j, h])        j ascending
+// The phases communicate through the stream order only: a dependency inside
+// one launch would need an agent-scope release/acquire per item, and on a
+// multi-XCD device those write back / invalidate a whole L2 each time.
 //
-// Fragment layout (v_mfma_f32_16x16x32_bf16, A = tokens 16 x 32, B = weights
-// 32 x 16): lane l supplies row/column (l & 15) and 8 reduction elements of
-// its lane group g = l >> 4.  One 16-byte load per lane of a packed INT4 row
-// holds 32 consecutive K values: lane group g of a 128-wide K block loads the
-// 32 values [32g, 32g + 32), which feed 4 MFMA steps (8 values each).  The A
-// fragments are loaded with the same K assignment, so the products pair up.
+// Workgroup: 4 compute waves + 1 staging wave.  The staging wave copies the
+// token rows of the current 128-wide K chunk into LDS (double buffered, one
+// barrier per chunk); each compute wave owns two 16-row weight tiles (G1: the
+// gate and up rows of the same 16 features, so SwiGLU is lane-local; G2: 32
+// output rows) over the full K and keeps kDepth chunks of its packed weights
+// in flight in registers.  The staging loads sit in another wave's memory
+// counter, so waiting for them never drains the weight prefetch.
+//
+// Weight arithmetic (per 128-wide K chunk, lane group g holds K [32g, 32g+32)):
+//   default: B = bf16_rne(fp32(q) * s), computed as fma(q + 2^(b-1), s,
+//     -2^(b-1) s) (one rounding, as fp32(q) * s) then RNE to bf16 -- the
+//     reference's dequantized BF16 weight bit for bit, for any group length
+//     % 32 == 0.  The layer is then the reference's dequantize-then-matmul up
+//     to the fp32 summation order.
+//   folded (LQ_MOE_FOLDED_SCALES): B = bf16(q + c), an exact small integer
+//     (INT4: c = 136, one AND-OR per two values; INT8: c = 128); the chunk's
+//     MFMA sum S = sum x*(q + c) and X = sum x (an MFMA against ones) give
+//     sum x*q = S - c X, scaled in fp32 by the group scale: the products use
+//     q * s without rounding each weight to bf16, which moves the output by
+//     about the reference tolerance (mean-relative ~5e-3), so it is opt-in.
+// Both feed the same K order to A and B: within each 8-value MFMA slot the K
+// order is [0,4,1,5,2,6,3,7]; the staging wave permutes the token rows to
+// match.
+#include <type_traits>
+
 #include "lq_common.h"
 #include "lq_route.h"
 
@@ -33,315 +52,633 @@ namespace lq {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+// a plain vector type (not HIP's uint4 struct) so staged copies stay in registers
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 256;  // 4 waves
-constexpr int kCols = 8;       // column tiles of 16 weight rows per workgroup
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kRowsMax = 32;                    // token rows per item (2 row tiles)
+constexpr int kKC = 128;                        // K per pipeline chunk
+constexpr int kRowBytes = kKC * 2;              // one staged row of a chunk (bf16)
+constexpr int kStageBytes = kRowsMax * kRowBytes;  // one LDS stage
+constexpr int kStages = 2;                      // LDS stages (double buffer)
+constexpr int kF1 = 64;                         // G1 features per item (128 weight rows)
+constexpr int kR2 = 128;                        // G2 output rows per item
+constexpr int kCombineBlock = 256;             // combine: 8 outputs per thread
 
-struct MoeArgs {
-  const uint16_t *x;        // [T, H] bf16
-  const int8_t *q1;         // [E, 2I, H] int8 or [E, 2I, H/2] packed
-  const float *s1;          // [E, 2I, ng1]
-  const int8_t *q2;         // [E, H, I] or [E, H, I/2]
-  const float *s2;          // [E, H, ng2]
-  const int32_t *ids;       // [T*k]
-  const float *topk_w;      // [T*k]
-  const int32_t *sorted;    // [N] assignment ids by expert
-  const int32_t *units;     // [max_units][3] (expert, first sorted position, rows)
-  const int32_t *n_units;   // [1]
-  uint16_t *act;            // [N, I] bf16, by sorted position
-  float *ybuf;              // [N, H] fp32, by assignment
-  uint16_t *out;            // [T, H] bf16
-  int64_t T;
-  int H, I, E, k;
-  int g1, ng1, g2, ng2;     // effective group length and groups per row
+// weight chunks in flight per compute wave: deeper for the bandwidth-bound
+// single-row-tile blocks, shallower where two row tiles of accumulators are live
+template <int NRT>
+constexpr int depth_for() {
+  return NRT == 1 ? 4 : 2;
+}
+
+struct alignas(16) PlanHeader {
+  int32_t ticket[2];  // next G1 / G2 item to hand out
+  int32_t n_g1;       // G1 items (items[0 .. n_g1))
+  int32_t n_g2;       // G2 items (items[n_g1 .. n_g1 + n_g2))
 };
 
-// torch's fp32 -> bf16 rounding, back to fp32
-__device__ __forceinline__ float bf16_round(float v) {
-  return __uint_as_float(static_cast<uint32_t>(f32_to_bf16_bits(v)) << 16);
+struct MoeArgs {
+  const uint16_t *xperm;   // [T, H] bf16, K slots permuted (kslot)
+  const int8_t *q1;        // [E, 2I, H] int8 or [E, 2I, H/2] packed
+  const float *s1;         // [E, 2I, ng1]
+  const int8_t *q2;        // [E, H, I] or [E, H, I/2]
+  const float *s2;         // [E, H, ng2]
+  const int32_t *ids;      // [T*k]
+  const float *topk_w;     // [T*k]
+  const int32_t *offsets;  // [E+1]
+  const int32_t *sorted;   // [T*k] assignment ids by expert
+  const uint2 *items;      // work list
+  PlanHeader *hdr;
+  uint16_t *act;           // [T*k, I] bf16, by sorted row
+  float *ybuf;             // [T*k, H] fp32, by assignment
+  uint16_t *out;           // [T, H] bf16
+  int64_t T;
+  int H, I, E, k;
+  int g1, ng1, g2, ng2;    // group length and groups per row of w1 / w2
+};
+
+// work item: x = slice << 8 | expert, y = row block
+__device__ __forceinline__ uint2 item_code(uint32_t e, uint32_t slice, uint32_t blk) {
+  return make_uint2((slice << 8) | e, blk);
 }
 
-// 8 INT4 values (value j in nibble j of w) -> bf16(fp32(q) * s)
-__device__ __forceinline__ bf16x8 deq_int4x8(uint32_t w, float s) {
-  bf16x8 r;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int32_t n = static_cast<int32_t>(w << (28 - 4 * j)) >> 28;
-    r[j] = static_cast<__bf16>(static_cast<float>(n) * s);
-  }
+// ---------------------------------------------------------------------------
+// weights -> MFMA B fragments (8 bf16 in K slot order [0,4,1,5,2,6,3,7])
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ uint32_t cvt2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2){lo, hi}, bf16x2));
+}
+
+// INT4 folded: 8 nibbles of w -> bf16(128 + (q + 8)) = 136 + q, exact; (q ^ 8) is q + 8
+__device__ __forceinline__ uint4 b_int4_folded(uint32_t w) {
+  const uint32_t v = w ^ 0x88888888u;
+  uint4 r;
+  r.x = (v & 0x000F000Fu) | 0x43004300u;
+  r.y = ((v >> 4) & 0x000F000Fu) | 0x43004300u;
+  r.z = ((v >> 8) & 0x000F000Fu) | 0x43004300u;
+  r.w = ((v >> 12) & 0x000F000Fu) | 0x43004300u;
   return r;
 }
 
-// 8 INT8 values (little-endian bytes of lo, hi) -> bf16(fp32(q) * s)
-__device__ __forceinline__ bf16x8 deq_int8x8(uint32_t lo, uint32_t hi, float s) {
-  bf16x8 r;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint32_t w = j < 4 ? lo : hi;
-    const int32_t n = static_cast<int32_t>(w << (24 - 8 * (j & 3))) >> 24;
-    r[j] = static_cast<__bf16>(static_cast<float>(n) * s);
-  }
-  return r;
+// INT4 exact: bf16_rne(fp32(q) * s), same slot order.  With n = q + 8
+// (nibble ^ 8): fma(n, s, -8s) rounds (n - 8) s once, exactly as fp32(q) * s
+// does; the high nibbles stay in place (16 n) and use s16 = s / 16 (exact).
+// c = -8 s.
+__device__ __forceinline__ uint4 b_int4_exact(uint32_t w, float s, float s16, float c) {
+  const uint32_t v = w ^ 0x88888888u;
+  const uint32_t lo = v & 0x0F0F0F0Fu;  // n of elements 0, 2, 4, 6
+  const uint32_t hi = v & 0xF0F0F0F0u;  // 16 n of elements 1, 3, 5, 7
+  const float e0 = fmaf(static_cast<float>(lo & 0xFF), s, c);
+  const float e2 = fmaf(static_cast<float>((lo >> 8) & 0xFF), s, c);
+  const float e4 = fmaf(static_cast<float>((lo >> 16) & 0xFF), s, c);
+  const float e6 = fmaf(static_cast<float>(lo >> 24), s, c);
+  const float e1 = fmaf(static_cast<float>(hi & 0xFF), s16, c);
+  const float e3 = fmaf(static_cast<float>((hi >> 8) & 0xFF), s16, c);
+  const float e5 = fmaf(static_cast<float>((hi >> 16) & 0xFF), s16, c);
+  const float e7 = fmaf(static_cast<float>(hi >> 24), s16, c);
+  return make_uint4(cvt2(e0, e4), cvt2(e1, e5), cvt2(e2, e6), cvt2(e3, e7));
+}
+
+// INT8: elements 0-3 in d0, 4-7 in d1 (little-endian bytes)
+__device__ __forceinline__ uint4 b_int8_folded(uint32_t d0, uint32_t d1) {
+  const uint32_t u = d0 ^ 0x80808080u, v = d1 ^ 0x80808080u;  // q + 128
+  return make_uint4(cvt2(static_cast<float>(u & 0xFF), static_cast<float>(v & 0xFF)),
+                    cvt2(static_cast<float>((u >> 8) & 0xFF), static_cast<float>((v >> 8) & 0xFF)),
+                    cvt2(static_cast<float>((u >> 16) & 0xFF), static_cast<float>((v >> 16) & 0xFF)),
+                    cvt2(static_cast<float>(u >> 24), static_cast<float>(v >> 24)));
+}
+
+__device__ __forceinline__ uint4 b_int8_exact(uint32_t d0, uint32_t d1, float s, float c) {
+  const uint32_t u = d0 ^ 0x80808080u, v = d1 ^ 0x80808080u;
+  auto f = [&](uint32_t byte) { return fmaf(static_cast<float>(byte), s, c); };
+  return make_uint4(cvt2(f(u & 0xFF), f(v & 0xFF)), cvt2(f((u >> 8) & 0xFF), f((v >> 8) & 0xFF)),
+                    cvt2(f((u >> 16) & 0xFF), f((v >> 16) & 0xFF)), cvt2(f(u >> 24), f(v >> 24)));
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
-// Packed weight bytes of one lane for one 128-wide K block (4 chunks of 32):
-// INT4: 16 bytes; INT8: 32 bytes.
+
+__device__ __forceinline__ float bf16_round(float v) {
+  return __uint_as_float(static_cast<uint32_t>(f32_to_bf16_bits(v)) << 16);
+}
+
+// packed weight bytes of one lane for one 128-wide K chunk of one tile
 template <int BITS>
-struct BFrag;
+struct WChunk;
 template <>
-struct BFrag<4> {
+struct WChunk<4> {
   uint4 v;
 };
 template <>
-struct BFrag<8> {
+struct WChunk<8> {
   uint4 v0, v1;
 };
 
-template <int BITS, int NRT, bool FIRST>
-__global__ __launch_bounds__(kThreads) void moe_gemm_kernel(MoeArgs a) {
-  __shared__ float red[4][kCols][4][64];  // split-K partials, one row tile
+// ---------------------------------------------------------------------------
+// one G1 / G2 item
+// ---------------------------------------------------------------------------
 
-  const int nunits = *a.n_units;
-  const int ntiles = FIRST ? (a.I >> 6) : (a.H >> 7);
-  const int total = nunits * ntiles;
-  const int bid = blockIdx.x;
-  if (bid >= total) return;
-  // blocks are dealt to the 8 XCDs round-robin (block b -> XCD b % 8); give
-  // each XCD a contiguous range of logical tiles so the tiles that share a
-  // unit's activations or an expert's weights share an L2
-  const int xcd = bid & 7, idx = bid >> 3;
-  const int per = total >> 3, rem = total & 7;
-  const int L = xcd * per + min(xcd, rem) + idx;
-  const int u = L / ntiles;
-  const int nt = L - u * ntiles;
-
-  const int e = a.units[3 * u];
-  const int row0 = a.units[3 * u + 1];
-  const int rows = a.units[3 * u + 2];
-  const int nrt = (rows + 15) >> 4;
-
-  const int K = FIRST ? a.H : a.I;
-  const int64_t rowbytes = BITS == 4 ? (K >> 1) : K;
-  const int nrows_w = FIRST ? 2 * a.I : a.H;
-  const int G = FIRST ? a.g1 : a.g2;
-  const int ng = FIRST ? a.ng1 : a.ng2;
-  const int8_t *W = (FIRST ? a.q1 : a.q2) + static_cast<int64_t>(e) * nrows_w * rowbytes;
-  const float *S = (FIRST ? a.s1 : a.s2) + static_cast<int64_t>(e) * nrows_w * ng;
-
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+template <int BITS, bool FOLDED, int NRT, bool FIRST>
+__device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, int row0, int rows,
+                                          unsigned char *lds) {
+  constexpr int kDepth = depth_for<NRT>();
+  static_assert(kDepth == 2 || kDepth == 4, "the K loop is unrolled for depth 2 or 4");
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
   const int lc = lane & 15;
   const int lg = lane >> 4;
+  const int K = FIRST ? a.H : a.I;
+  const int nk = (K + kKC - 1) / kKC;
 
-  const int8_t *wrow[kCols];
-  const float *srow[kCols];
+  // ---- staging (all four waves): a chunk is NRT*16 rows x 16 chunks of 16
+  // bytes; wave w, lane l owns pieces w*64 + l + 256q (q < NRT): row
+  // (w*64 + l + 256q) >> 4, 16-byte chunk c = l & 15, stored at LDS slot
+  // c ^ (row & 15) of the row (XOR swizzle: conflict-free fragment reads).
+  // Rows arrive already K-slot permuted (xperm, act).  A chunk is loaded into
+  // registers two steps before it is consumed and written to LDS one step
+  // before, so these loads never stall the weight prefetch.
+  const uint16_t *abase = FIRST ? a.xperm : a.act;
+  int srcoff[NRT];  // element offset of each owned row (row 0 for padding rows)
+  int ldsoff[NRT];  // byte offset of each owned piece within a stage
 #pragma unroll
-  for (int c = 0; c < kCols; ++c) {
-    const int r = FIRST ? ((c < 4 ? 0 : a.I) + nt * 64 + 16 * (c & 3) + lc) : (nt * 128 + 16 * c + lc);
-    wrow[c] = W + static_cast<int64_t>(r) * rowbytes;
-    srow[c] = S + static_cast<int64_t>(r) * ng;
+  for (int q = 0; q < NRT; ++q) {
+    const int piece = wave * 64 + lane + 256 * q;
+    const int r = piece >> 4;
+    const int rr = r < rows ? r : 0;
+    srcoff[q] = (FIRST ? (a.sorted[row0 + rr] / a.k) * a.H : (row0 + rr) * a.I) + 8 * (lane & 15);
+    ldsoff[q] = r * kRowBytes + 16 * ((lane & 15) ^ (r & 15));
   }
-  const uint16_t *arow[NRT];
+  auto load_a = [&](int i, u32x4(&v)[NRT]) __attribute__((always_inline)) {
 #pragma unroll
-  for (int rt = 0; rt < NRT; ++rt) {
-    const int m = rt * 16 + lc;
-    const int pos = row0 + (m < rows ? m : 0);
-    arow[rt] = FIRST ? a.x + static_cast<int64_t>(a.sorted[pos] / a.k) * a.H
-                     : a.act + static_cast<int64_t>(pos) * a.I;
+    for (int q = 0; q < NRT; ++q) {
+      int kk = i * kKC;
+      // K tail: the chunk is past the row end; any finite in-row value (its B is zero)
+      kk = kk + 8 * (lane & 15) < K ? kk : K - 8 - 8 * (lane & 15);
+      v[q] = *reinterpret_cast<const u32x4 *>(abase + srcoff[q] + kk);
+    }
+  };
+  auto store_a = [&](int i, const u32x4(&v)[NRT]) __attribute__((always_inline)) {
+    unsigned char *buf = lds + (i % kStages) * kStageBytes;
+#pragma unroll
+    for (int q = 0; q < NRT; ++q) *reinterpret_cast<u32x4 *>(buf + ldsoff[q]) = v[q];
+  };
+
+  // ---- weights: wave w owns two 16-row tiles
+  const int64_t rowbytes = BITS == 4 ? (K >> 1) : K;
+  const int G = FIRST ? a.g1 : a.g2;
+  const int ng = FIRST ? a.ng1 : a.ng2;
+  const int nrows_w = FIRST ? 2 * a.I : a.H;
+  const int8_t *W = (FIRST ? a.q1 : a.q2) + static_cast<int64_t>(e) * nrows_w * rowbytes;
+  const float *S = (FIRST ? a.s1 : a.s2) + static_cast<int64_t>(e) * nrows_w * ng;
+  int wr[2];
+  if (FIRST) {
+    wr[0] = slice * kF1 + 16 * wave + lc;        // gate row
+    wr[1] = a.I + slice * kF1 + 16 * wave + lc;  // up row of the same feature
+  } else {
+    wr[0] = slice * kR2 + 32 * wave + lc;
+    wr[1] = wr[0] + 16;
   }
+  const int8_t *wp[2] = {W + wr[0] * rowbytes, W + wr[1] * rowbytes};
+  const float *sp[2] = {S + static_cast<int64_t>(wr[0]) * ng, S + static_cast<int64_t>(wr[1]) * ng};
 
-  floatx4 acc[NRT][kCols];
+  auto load_w = [&](int i, WChunk<BITS>(&w)[2], float(&sc)[2]) __attribute__((always_inline)) {
+    const int kelem = i * kKC + 32 * lg;
+    const bool ok = kelem < K;
+    const int ke = ok ? kelem : 0;  // K tail: a valid address, the value is discarded
+    const int sidx = (FOLDED ? i * kKC : ke) / G;
 #pragma unroll
-  for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-    for (int c = 0; c < kCols; ++c) acc[rt][c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-
-  // this wave's range of 32-wide K chunks
-  const int nck = K >> 5;
-  const int c0 = (wave * nck) >> 2;
-  const int c1 = ((wave + 1) * nck) >> 2;
-  int kc = c0;
-
-  auto load_b = [&](int kchunk, BFrag<BITS>(&b)[kCols], float(&s)[kCols]) {
-    const int kelem = 32 * (kchunk + lg);  // first K element of this lane group
-#pragma unroll
-    for (int c = 0; c < kCols; ++c) {
+    for (int c = 0; c < 2; ++c) {
       if constexpr (BITS == 4) {
-        b[c].v = *reinterpret_cast<const uint4 *>(wrow[c] + (kelem >> 1));
+        w[c].v = *reinterpret_cast<const uint4 *>(wp[c] + (ke >> 1));
       } else {
-        const uint4 *p = reinterpret_cast<const uint4 *>(wrow[c] + kelem);
-        b[c].v0 = p[0];
-        b[c].v1 = p[1];
+        const uint4 *p = reinterpret_cast<const uint4 *>(wp[c] + ke);
+        w[c].v0 = p[0];
+        w[c].v1 = p[1];
       }
-      s[c] = srow[c][kelem / G];
+      sc[c] = sp[c][sidx];
     }
   };
 
-  if (kc + 4 <= c1) {
-    BFrag<BITS> bcur[kCols];
-    float scur[kCols];
-    load_b(kc, bcur, scur);
-    for (; kc + 4 <= c1; kc += 4) {
-      BFrag<BITS> bnxt[kCols];
-      float snxt[kCols];
-      const bool more = kc + 8 <= c1;
-      if (more) load_b(kc + 4, bnxt, snxt);
-      uint4 af[NRT][4];
+  floatx4 tot[NRT][2];
+#pragma unroll
+  for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) tot[rt][c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // one 128-wide K chunk of this wave's two tiles against the staged rows;
+  // TAIL: the chunk may run past K (K % 128 != 0), lanes past it feed zeros
+  auto compute = [&](int i, const WChunk<BITS>(&w)[2], const float(&sc)[2], auto tail_tag)
+      __attribute__((always_inline)) {
+    constexpr bool TAIL = decltype(tail_tag)::value;
+    const unsigned char *buf = lds + (i % kStages) * kStageBytes;
+    const bool kvalid = !TAIL || i * kKC + 32 * lg < K;
+    constexpr float kOff = BITS == 4 ? 8.0f : 128.0f;
+    const uint32_t one2 = kvalid ? 0x3F803F80u : 0u;  // bf16 1.0 pairs; zero past the K tail
+    const uint4 ones4 = make_uint4(one2, one2, one2, one2);
+    floatx4 acc[NRT][2];
+    floatx4 xs[NRT];
+    float cexact[2], s16[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      cexact[c] = -kOff * sc[c];
+      s16[c] = sc[c] * 0.0625f;
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      uint4 b[2];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        if constexpr (BITS == 4) {
+          const uint32_t q = s == 0 ? w[c].v.x : s == 1 ? w[c].v.y : s == 2 ? w[c].v.z : w[c].v.w;
+          b[c] = FOLDED ? b_int4_folded(q) : b_int4_exact(q, sc[c], s16[c], cexact[c]);
+        } else {
+          const uint4 &v = s < 2 ? w[c].v0 : w[c].v1;
+          const uint32_t d0 = (s & 1) ? v.z : v.x;
+          const uint32_t d1 = (s & 1) ? v.w : v.y;
+          b[c] = FOLDED ? b_int8_folded(d0, d1) : b_int8_exact(d0, d1, sc[c], cexact[c]);
+        }
+        if constexpr (TAIL) {
+          if (!kvalid) b[c] = make_uint4(0, 0, 0, 0);
+        }
+      }
 #pragma unroll
       for (int rt = 0; rt < NRT; ++rt) {
-        if (rt < nrt) {
-          const uint4 *p = reinterpret_cast<const uint4 *>(arow[rt] + 32 * (kc + lg));
+        // row rt*16 + lc (its low 4 bits are lc), K chunk 4*lg + s of this 128-wide chunk
+        const uint4 af = *reinterpret_cast<const uint4 *>(buf + (rt * 16 + lc) * kRowBytes +
+                                                          16 * ((4 * lg + s) ^ lc));
+        if constexpr (!FOLDED) {
 #pragma unroll
-          for (int s = 0; s < 4; ++s) af[rt][s] = p[s];
-        }
-      }
+          for (int c = 0; c < 2; ++c)
+            tot[rt][c] =
+                __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(af), as_bf16x8(b[c]), tot[rt][c], 0, 0, 0);
+        } else {
+          const floatx4 z = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int c = 0; c < kCols; ++c) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          bf16x8 b;
-          if constexpr (BITS == 4) {
-            const uint32_t w = s == 0 ? bcur[c].v.x : s == 1 ? bcur[c].v.y : s == 2 ? bcur[c].v.z : bcur[c].v.w;
-            b = deq_int4x8(w, scur[c]);
-          } else {
-            const uint4 &v = s < 2 ? bcur[c].v0 : bcur[c].v1;
-            const uint32_t lo = (s & 1) ? v.z : v.x;
-            const uint32_t hi = (s & 1) ? v.w : v.y;
-            b = deq_int8x8(lo, hi, scur[c]);
-          }
-#pragma unroll
-          for (int rt = 0; rt < NRT; ++rt)
-            if (rt < nrt)
-              acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(af[rt][s]), b, acc[rt][c], 0, 0, 0);
-        }
-      }
-      if (more) {
-#pragma unroll
-        for (int c = 0; c < kCols; ++c) {
-          bcur[c] = bnxt[c];
-          scur[c] = snxt[c];
+          for (int c = 0; c < 2; ++c)
+            acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(af), as_bf16x8(b[c]),
+                                                                 s == 0 ? z : acc[rt][c], 0, 0, 0);
+          xs[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(af), as_bf16x8(ones4), s == 0 ? z : xs[rt],
+                                                           0, 0, 0);
         }
       }
     }
-  }
-  // remaining single 32-wide chunks: lane group g takes values [8g, 8g + 8)
-  for (; kc < c1; ++kc) {
-    const int kelem = 32 * kc + 8 * lg;
-    uint4 af[NRT];
-#pragma unroll
-    for (int rt = 0; rt < NRT; ++rt)
-      if (rt < nrt) af[rt] = *reinterpret_cast<const uint4 *>(arow[rt] + kelem);
-#pragma unroll
-    for (int c = 0; c < kCols; ++c) {
-      const float sc = srow[c][(32 * kc) / G];
-      bf16x8 b;
-      if constexpr (BITS == 4) {
-        b = deq_int4x8(*reinterpret_cast<const uint32_t *>(wrow[c] + (kelem >> 1)), sc);
-      } else {
-        const uint2 v = *reinterpret_cast<const uint2 *>(wrow[c] + kelem);
-        b = deq_int8x8(v.x, v.y, sc);
-      }
+    if constexpr (FOLDED) {
+      // sum x*q = S - bias * X, then the column's group scale
+      constexpr float kBias = BITS == 4 ? 136.0f : 128.0f;
 #pragma unroll
       for (int rt = 0; rt < NRT; ++rt)
-        if (rt < nrt) acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(af[rt]), b, acc[rt][c], 0, 0, 0);
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            tot[rt][c][j] = fmaf(sc[c], fmaf(-kBias, xs[rt][j], acc[rt][c][j]), tot[rt][c][j]);
+    }
+  };
+
+  // Issue order per step i: A(i+2) into registers, compute chunk i, weights
+  // of chunk i+D, A(i+1) registers -> LDS, barrier.
+  WChunk<BITS> wb[kDepth][2];
+  float sb[kDepth][2];
+#pragma unroll
+  for (int d = 0; d < kDepth; ++d)
+    if (d < nk) load_w(d, wb[d], sb[d]);
+  u32x4 av[2][NRT];
+  load_a(0, av[0]);
+  if (nk > 1) load_a(1, av[1]);
+  store_a(0, av[0]);
+  __syncthreads();  // chunk 0 staged
+
+  // One K step: stage A(i+2), compute chunk i, prefetch weights of chunk
+  // i+D, write A(i+1) to LDS.  In the steady state every load is issued
+  // unconditionally (straight-line code lets the compiler count the memory
+  // operations still in flight exactly instead of draining them); the last
+  // steps run the guarded form.  (kDepth is even, so step parity = d parity
+  // and the register buffers are static.)
+  auto step = [&](int i, auto d_tag, auto steady_tag) __attribute__((always_inline)) {
+    constexpr int d = decltype(d_tag)::value;
+    constexpr bool steady = decltype(steady_tag)::value;
+    if (steady || i + 2 < nk) load_a(i + 2, av[d & 1]);
+    if (steady || (K % kKC) == 0 || i + 1 < nk)
+      compute(i, wb[d], sb[d], std::false_type{});
+    else
+      compute(i, wb[d], sb[d], std::true_type{});  // the partial last chunk
+    if (steady || i + kDepth < nk) load_w(i + kDepth, wb[d], sb[d]);
+    if (steady || i + 1 < nk) store_a(i + 1, av[(d + 1) & 1]);
+    __syncthreads();  // chunk i consumed by every wave, chunk i + 1 staged
+  };
+  int i0 = 0;
+  // steady blocks: every step of the block has i + kDepth < nk (and so i + 2 < nk)
+  for (; i0 + 2 * kDepth - 1 < nk; i0 += kDepth) {
+    step(i0 + 0, std::integral_constant<int, 0>{}, std::true_type{});
+    step(i0 + 1, std::integral_constant<int, 1>{}, std::true_type{});
+    if constexpr (kDepth > 2) {
+      step(i0 + 2, std::integral_constant<int, 2>{}, std::true_type{});
+      step(i0 + 3, std::integral_constant<int, 3>{}, std::true_type{});
+    }
+  }
+  for (; i0 < nk; i0 += kDepth) {
+    step(i0 + 0, std::integral_constant<int, 0>{}, std::false_type{});
+    if (i0 + 1 < nk) step(i0 + 1, std::integral_constant<int, 1>{}, std::false_type{});
+    if constexpr (kDepth > 2) {
+      if (i0 + 2 < nk) step(i0 + 2, std::integral_constant<int, 2>{}, std::false_type{});
+      if (i0 + 3 < nk) step(i0 + 3, std::integral_constant<int, 3>{}, std::false_type{});
     }
   }
 
-  // split-K reduction and epilogue, one row tile at a time
+  if constexpr (FIRST) {
+    // reference op order (INFERENCE_REPO_CHANGES.md:296-309): g, u -> bf16;
+    // silu in fp32 -> bf16; bf16 product.  act is stored K-slot permuted for
+    // the G2 items that stage it.
+    const int f = kslot(slice * kF1 + 16 * wave + lc);
 #pragma unroll
-  for (int rt = 0; rt < NRT; ++rt) {
-    if (rt >= nrt) break;
-    __syncthreads();
+    for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
-    for (int c = 0; c < kCols; ++c)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) red[wave][c][r][lane] = acc[rt][c][r];
-    __syncthreads();
-    if constexpr (FIRST) {
-      // 16 rows x 64 features: thread -> feature j, rows 4q .. 4q+3
-      const int j = threadIdx.x & 63;
-      const int q = threadIdx.x >> 6;
-      const int c = j >> 4;
-      const int src = q * 16 + (j & 15);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = rt * 16 + 4 * q + r;
-        const float g = ((red[0][c][r][src] + red[1][c][r][src]) + red[2][c][r][src]) + red[3][c][r][src];
-        const float up =
-            ((red[0][c + 4][r][src] + red[1][c + 4][r][src]) + red[2][c + 4][r][src]) + red[3][c + 4][r][src];
+      for (int j = 0; j < 4; ++j) {
+        const int m = rt * 16 + 4 * lg + j;
         if (m < rows) {
-          // reference op order: g, u -> bf16; silu in fp32 -> bf16; bf16 product
-          const float gb = bf16_round(g);
-          const float ub = bf16_round(up);
-          const float sb = bf16_round(gb / (1.0f + expf(-gb)));
-          a.act[static_cast<int64_t>(row0 + m) * a.I + nt * 64 + j] = f32_to_bf16_bits(sb * ub);
+          const float gb = bf16_round(tot[rt][0][j]);
+          const float ub = bf16_round(tot[rt][1][j]);
+          const float sb16 = bf16_round(gb / (1.0f + __expf(-gb)));
+          a.act[static_cast<int64_t>(row0 + m) * a.I + f] = f32_to_bf16_bits(sb16 * ub);
         }
       }
-    } else {
-      // 16 rows x 128 features: thread -> feature j, rows 8h .. 8h+7
-      const int j = threadIdx.x & 127;
-      const int h = threadIdx.x >> 7;
-      const int c = j >> 4;
+  } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int grp = 2 * h + (i >> 2);
-        const int r = i & 3;
-        const int src = grp * 16 + (j & 15);
-        const int m = rt * 16 + 4 * grp + r;
-        const float y = ((red[0][c][r][src] + red[1][c][r][src]) + red[2][c][r][src]) + red[3][c][r][src];
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int m = rt * 16 + 4 * lg + j;
         if (m < rows) {
           const int asg = a.sorted[row0 + m];
-          a.ybuf[static_cast<int64_t>(asg) * a.H + nt * 128 + j] = y * a.topk_w[asg];
+          const float wt = a.topk_w[asg];
+          float *yrow = a.ybuf + static_cast<int64_t>(asg) * a.H;
+          yrow[wr[0]] = tot[rt][0][j] * wt;
+          yrow[wr[1]] = tot[rt][1][j] * wt;
         }
       }
-    }
   }
 }
 
-// out[t, h] = bf16(sum_j y[t*k + j, h]) over the routed slots, j ascending
-__global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ ybuf, const int32_t *__restrict__ ids,
-                                                      int64_t T, int H, int k, int E, uint16_t *__restrict__ out) {
-  const int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int hq = H >> 2;
-  if (q >= T * hq) return;
-  const int64_t t = q / hq;
-  const int h = static_cast<int>(q - t * hq) << 2;
-  float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+template <int BITS, bool FOLDED, bool FIRST>
+__device__ __forceinline__ void gemm_dispatch(const MoeArgs &a, int e, int slice, int row0, int rows,
+                                              unsigned char *lds) {
+  if (rows <= 16)
+    gemm_item<BITS, FOLDED, 1, FIRST>(a, e, slice, row0, rows, lds);
+  else
+    gemm_item<BITS, FOLDED, 2, FIRST>(a, e, slice, row0, rows, lds);
+}
+
+// out[t, h..h+8) = bf16(sum_j y[t*k + j, h..h+8)) over the routed slots, j ascending
+__global__ __launch_bounds__(kCombineBlock) void combine_kernel(const float *__restrict__ ybuf,
+                                                                const int32_t *__restrict__ ids, int64_t T,
+                                                                int H, int k, int E, uint16_t *__restrict__ out) {
+  const int64_t base = (static_cast<int64_t>(blockIdx.x) * kCombineBlock + threadIdx.x) * 8;
+  if (base >= T * H) return;
+  const int64_t t = base / H;
+  const int h = static_cast<int>(base - t * H);
+  float s[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
   for (int j = 0; j < k; ++j) {
     const int id = ids[t * k + j];
     if (id < 0 || id >= E) continue;
-    const float4 v = *reinterpret_cast<const float4 *>(ybuf + (t * k + j) * H + h);
-    s.x += v.x;
-    s.y += v.y;
-    s.z += v.z;
-    s.w += v.w;
+    const float4 *y = reinterpret_cast<const float4 *>(ybuf + (t * k + j) * H + h);
+    const float4 v0 = y[0], v1 = y[1];
+    s[0] += v0.x;
+    s[1] += v0.y;
+    s[2] += v0.z;
+    s[3] += v0.w;
+    s[4] += v1.x;
+    s[5] += v1.y;
+    s[6] += v1.z;
+    s[7] += v1.w;
   }
-  const uint32_t lo = f32_to_bf16_bits(s.x) | (static_cast<uint32_t>(f32_to_bf16_bits(s.y)) << 16);
-  const uint32_t hi = f32_to_bf16_bits(s.z) | (static_cast<uint32_t>(f32_to_bf16_bits(s.w)) << 16);
-  *reinterpret_cast<uint2 *>(out + t * H + h) = make_uint2(lo, hi);
+  uint32_t p[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    p[i] = static_cast<uint32_t>(f32_to_bf16_bits(s[2 * i])) |
+           (static_cast<uint32_t>(f32_to_bf16_bits(s[2 * i + 1])) << 16);
+  *reinterpret_cast<uint4 *>(out + base) = make_uint4(p[0], p[1], p[2], p[3]);
 }
 
+// Persistent G1 (FIRST) or G2 kernel: each workgroup takes items of its phase
+// in ticket order until the phase's list is exhausted.
+template <int BITS, bool FOLDED, bool FIRST>
+__global__ __launch_bounds__(kThreads, 2) void moe_gemm_kernel(MoeArgs a) {
+  __shared__ __align__(16) unsigned char lds[kStages * kStageBytes];
+  __shared__ int s_item;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int n_items = __builtin_amdgcn_readfirstlane(FIRST ? a.hdr->n_g1 : a.hdr->n_g2);
+  const uint2 *items = a.items + (FIRST ? 0 : __builtin_amdgcn_readfirstlane(a.hdr->n_g1));
+  int32_t *ticket = &a.hdr->ticket[FIRST ? 0 : 1];
+  // Every branch of this loop is wave-uniform.  (A lane-divergent
+  // `if (tid == 0)` here lets the compiler split the loop so that lanes
+  // other than 0 re-enter the item body without a new ticket.)
+  for (;;) {
+    if (wave == 0) {
+      // lane 0 takes the ticket; the other lanes add 0 and read the same word
+      const int mine = __hip_atomic_fetch_add(ticket, lane == 0 ? 1 : 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_item = __builtin_amdgcn_readfirstlane(mine);
+    }
+    __syncthreads();
+    // every value below is wave-uniform (scalar): the branches it feeds contain barriers
+    const int t = __builtin_amdgcn_readfirstlane(s_item);
+    __syncthreads();
+    if (t >= n_items) break;
+    const uint2 it = items[t];
+    const uint32_t ix = __builtin_amdgcn_readfirstlane(it.x);
+    const int e = static_cast<int>(ix & 0xFFu);
+    const int slice = static_cast<int>(ix >> 8);
+    const int blk = static_cast<int>(__builtin_amdgcn_readfirstlane(it.y));
+    const int row0 = __builtin_amdgcn_readfirstlane(a.offsets[e] + blk * kRowsMax);
+    const int rows = __builtin_amdgcn_readfirstlane(min(kRowsMax, a.offsets[e + 1] - row0));
+    gemm_dispatch<BITS, FOLDED, FIRST>(a, e, slice, row0, rows, lds);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// plan: stable permutation + work list (one workgroup)
+// ---------------------------------------------------------------------------
+
+constexpr int kPlanBlock = 1024;
+constexpr int kPlanWaves = kPlanBlock / 64;
+
+struct PlanArgs {
+  const int32_t *ids;
+  int64_t N;
+  int E;
+  int32_t *counts;
+  int32_t *offsets;
+  int32_t *sorted;
+  // work list (items == nullptr: permutation only)
+  uint2 *items;
+  PlanHeader *hdr;
+  int nf;  // G1 slices per expert (I / kF1)
+  int nr;  // G2 slices per expert (H / kR2)
+};
+
+// exclusive scan of in[0..E) by wave 0 (lane l owns entries 4l..4l+3)
+__device__ void wave0_exclusive_scan(const int *in, int *out, int E, int *total) {
+  const int lane = threadIdx.x & 63;
+  int v[4];
+  int local = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = 4 * lane + i;
+    v[i] = e < E ? in[e] : 0;
+    local += v[i];
+  }
+  int incl = local;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  int run = incl - local;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = 4 * lane + i;
+    if (e < E) out[e] = run;
+    run += v[i];
+  }
+  const int tot = __shfl(incl, 63, 64);
+  if (lane == 0) *total = tot;
+}
+
+__global__ __launch_bounds__(kPlanBlock) void plan_kernel(PlanArgs p) {
+  __shared__ int hist[kMaxExperts];
+  __shared__ int base[kMaxExperts];
+  __shared__ int nbs[kMaxExperts + 1];  // exclusive scan of row blocks per expert
+  __shared__ int wcnt[kPlanWaves][kMaxExperts];
+  __shared__ int total;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int E = p.E;
+  for (int e = tid; e < kMaxExperts; e += kPlanBlock) hist[e] = 0;
+  for (int i = tid; i < kPlanWaves * kMaxExperts; i += kPlanBlock) (&wcnt[0][0])[i] = 0;
+  __syncthreads();
+  for (int64_t a = tid; a < p.N; a += kPlanBlock) {
+    const int id = p.ids[a];
+    if (id >= 0 && id < E) atomicAdd(&hist[id], 1);
+  }
+  __syncthreads();
+  if (wave == 0) wave0_exclusive_scan(hist, base, E, &total);
+  __syncthreads();
+  for (int e = tid; e < E; e += kPlanBlock) {
+    p.counts[e] = hist[e];
+    p.offsets[e] = base[e];
+  }
+  if (tid == 0) p.offsets[E] = total;
+
+  if (p.items != nullptr) {
+    // row blocks per expert and their scan
+    for (int e = tid; e < E; e += kPlanBlock) wcnt[0][e] = (hist[e] + kRowsMax - 1) / kRowsMax;
+    __syncthreads();
+    if (wave == 0) wave0_exclusive_scan(wcnt[0], nbs, E, &nbs[E]);
+    __syncthreads();
+    const int nb_total = nbs[E];
+    const int n_g1 = nb_total * p.nf;
+    const int n_g2 = nb_total * p.nr;
+    const int n_items = n_g1 + n_g2;
+    for (int t = tid; t < n_items; t += kPlanBlock) {
+      const bool g1 = t < n_g1;
+      const int per = g1 ? p.nf : p.nr;
+      const int local = g1 ? t : t - n_g1;
+      const int bidx = local / per;  // global row-block index (expert-major)
+      int lo = 0, hi = E;            // largest e with nbs[e] <= bidx
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (nbs[mid] <= bidx) lo = mid;
+        else hi = mid;
+      }
+      const int e = lo;
+      const int nb = nbs[e + 1] - nbs[e];
+      const int within = local - nbs[e] * per;  // slice-major, block-minor
+      p.items[t] = item_code(e, within / nb, within % nb);
+    }
+    if (tid == 0) {
+      p.hdr->ticket[0] = 0;
+      p.hdr->ticket[1] = 0;
+      p.hdr->n_g1 = n_g1;
+      p.hdr->n_g2 = n_g2;
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += kPlanBlock) wcnt[0][e] = 0;
+  }
+  __syncthreads();
+
+  // stable scatter: chunks of kPlanBlock assignments in order; within a
+  // chunk, rank = peers with the same expert in lower lanes of this wave +
+  // peers in lower waves
+  int nbits = 1;
+  while ((1 << nbits) <= E) ++nbits;
+  const unsigned long long lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int64_t chunk = 0; chunk < p.N; chunk += kPlanBlock) {
+    const int64_t a = chunk + tid;
+    const int raw = a < p.N ? p.ids[a] : -1;
+    const bool valid = raw >= 0 && raw < E;
+    const int key = valid ? raw : E;
+    unsigned long long peers = ~0ull;
+    for (int b = 0; b < nbits; ++b) {
+      const bool bit = (key >> b) & 1;
+      const unsigned long long bal = __ballot(bit);
+      peers &= bit ? bal : ~bal;
+    }
+    const int rank = __popcll(peers & lt_mask);
+    if (valid && rank == 0) wcnt[wave][key] = __popcll(peers);
+    __syncthreads();
+    if (valid) {
+      int pos = base[key] + rank;
+      for (int w = 0; w < wave; ++w) pos += wcnt[w][key];
+      p.sorted[pos] = static_cast<int32_t>(a);
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += kPlanBlock) {
+      int s = 0;
+      for (int w = 0; w < kPlanWaves; ++w) {
+        s += wcnt[w][e];
+        wcnt[w][e] = 0;
+      }
+      base[e] += s;
+    }
+    __syncthreads();
+  }
+}
+
+// x [rows, H] -> xperm, each group of 8 bf16 in K-slot order (8 values per thread)
+__global__ __launch_bounds__(256) void permute_rows_kernel(const uint16_t *__restrict__ x, int64_t n8,
+                                                          uint16_t *__restrict__ xperm) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n8)
+    reinterpret_cast<uint4 *>(xperm)[i] = permute_kslots(reinterpret_cast<const uint4 *>(x)[i]);
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+
 struct WsLayout {
-  size_t counts, offsets, sorted, units, n_units, ids, weights, act, ybuf, total;
+  size_t counts, offsets, sorted, hdr, items, ids, weights, xperm, act, ybuf, total;
 };
 
 inline size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
-int unit_rows_for(int64_t N, int E) {
-  const int64_t avg = N / (E > 0 ? E : 1);
-  if (avg <= 16) return 16;
-  if (avg <= 32) return 32;
-  return 64;
+int64_t max_items_for(int64_t T, int H, int I, int E, int k) {
+  const int64_t N = T * k;
+  const int64_t blocks = std::min<int64_t>(E, N) + N / kRowsMax;
+  return blocks * (I / kF1 + H / kR2);
 }
-
-int64_t max_units_for(int64_t N, int E, int mc) { return E + N / mc; }
 
 WsLayout ws_layout(int64_t T, int H, int I, int E, int k) {
   const int64_t N = T * k;
-  const int mc = unit_rows_for(N, E);
   WsLayout w;
   size_t off = 0;
   auto take = [&](size_t &field, size_t bytes) {
@@ -351,26 +688,38 @@ WsLayout ws_layout(int64_t T, int H, int I, int E, int k) {
   take(w.counts, sizeof(int32_t) * E);
   take(w.offsets, sizeof(int32_t) * (E + 1));
   take(w.sorted, sizeof(int32_t) * N);
-  take(w.units, sizeof(int32_t) * 3 * max_units_for(N, E, mc));
-  take(w.n_units, sizeof(int32_t));
+  take(w.hdr, sizeof(PlanHeader));
+  take(w.items, sizeof(uint2) * max_items_for(T, H, I, E, k));
   take(w.ids, sizeof(int32_t) * N);
   take(w.weights, sizeof(float) * N);
+  take(w.xperm, sizeof(uint16_t) * T * H);
   take(w.act, sizeof(uint16_t) * N * I);
   take(w.ybuf, sizeof(float) * N * H);
   w.total = off;
   return w;
 }
 
-template <int BITS, int NRT>
-void launch_gemm1(const MoeArgs &a, int64_t max_units, hipStream_t st) {
-  moe_gemm_kernel<BITS, NRT, true><<<static_cast<int>(max_units * (a.I >> 6)), kThreads, 0, st>>>(a);
-}
-template <int BITS, int NRT>
-void launch_gemm2(const MoeArgs &a, int64_t max_units, hipStream_t st) {
-  moe_gemm_kernel<BITS, NRT, false><<<static_cast<int>(max_units * (a.H >> 7)), kThreads, 0, st>>>(a);
-}
-
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// persistent grid: resident workgroups of one GEMM kernel on this device
+template <int BITS, bool FOLDED, bool FIRST>
+int gemm_grid(int64_t max_items) {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int g = cached[dev];
+  if (g == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, moe_gemm_kernel<BITS, FOLDED, FIRST>, kThreads, 0) !=
+            hipSuccess ||
+        per_cu <= 0)
+      per_cu = 1;
+    g = cus * per_cu;
+    cached[dev] = g;
+  }
+  return static_cast<int>(std::min<int64_t>(g, std::max<int64_t>(max_items, 1)));
+}
 
 // Measurement hook (lq_moe_profile_events): caller-owned hipEvent_t handles
 // recorded on the call's stream at the kernel boundaries of the next layer
@@ -392,14 +741,15 @@ struct ProfileMarks {
 };
 
 int validate_layer(const void *x, int64_t T, int H, int I, int E, int k, const int8_t *q1, const float *s1,
-                   const int8_t *q2, const float *s2, int bits, int64_t group_w1, int64_t group_w2,
+                   const int8_t *q2, const float *s2, int bits, int64_t group_w1, int64_t group_w2, int flags,
                    void *workspace, size_t ws_bytes, void *out) {
   if (bits != 4 && bits != 8) return fail(LQ_ERR_VALUE, "bits must be 8 or 4, got " + std::to_string(bits));
   if (T < 0 || H <= 0 || I <= 0 || k <= 0) return fail(LQ_ERR_VALUE, "moe_forward: bad shape");
   if (E < 1 || E > kMaxExperts)
     return fail(LQ_ERR_UNSUPPORTED, "moe_forward: 1 <= num_experts <= " + std::to_string(kMaxExperts));
   if (k > E) return fail(LQ_ERR_VALUE, "moe_forward: top_k exceeds num_experts");
-  if (H % 128 != 0 || I % 64 != 0)
+  if (flags & ~LQ_MOE_FOLDED_SCALES) return fail(LQ_ERR_VALUE, "moe_forward: unknown flags");
+  if (H % kR2 != 0 || I % kF1 != 0)
     return fail(LQ_ERR_UNSUPPORTED, "moe_forward: needs hidden % 128 == 0 and intermediate % 64 == 0");
   const int64_t g1 = effective_group(H, group_w1);
   const int64_t g2 = effective_group(I, group_w2);
@@ -408,7 +758,10 @@ int validate_layer(const void *x, int64_t T, int H, int I, int E, int k, const i
                 "moe_forward: the group length along K must be a multiple of 32 (got " + std::to_string(g1) +
                     " for w1, " + std::to_string(g2) + " for w2)");
   const int64_t N = T * k;
-  if (N > 0x7FFFFFFF / (H > I ? H : I)) return fail(LQ_ERR_UNSUPPORTED, "moe_forward: too many tokens");
+  if (T > (int64_t{1} << 18) || N * static_cast<int64_t>(H > I ? H : I) > 0x7FFFFFFFll ||
+      T * static_cast<int64_t>(H) > 0x7FFFFFFFll)
+    return fail(LQ_ERR_UNSUPPORTED, "moe_forward: too many tokens for one call");
+  if (max_items_for(T, H, I, E, k) > 0x3FFFFFFF) return fail(LQ_ERR_UNSUPPORTED, "moe_forward: work list too long");
   if (T == 0) return LQ_OK;
   if (!x || !q1 || !s1 || !q2 || !s2 || !workspace || !out) return fail(LQ_ERR_VALUE, "moe_forward: null pointer");
   if (!aligned16(x) || !aligned16(q1) || !aligned16(q2) || !aligned16(workspace) || !aligned16(out))
@@ -420,29 +773,73 @@ int validate_layer(const void *x, int64_t T, int H, int I, int E, int k, const i
   return LQ_OK;
 }
 
-// permute -> GEMM1 -> GEMM2 -> combine, marks[first_mark ..] at each boundary
-int moe_forward_impl(const void *x, int64_t T, int H, int I, int E, int k, const int8_t *q1, const float *s1,
-                     const int8_t *q2, const float *s2, int bits, int64_t group_w1, int64_t group_w2,
-                     const int32_t *topk_ids, const float *topk_weights, char *ws, void *out, hipStream_t st,
-                     ProfileMarks &pm, int first_mark) {
+// G1 -> G2 -> combine, marks[first + 1 ..] after each
+template <int BITS, bool FOLDED>
+int launch_phases(const MoeArgs &a, int64_t max_g1, int64_t max_g2, hipStream_t st, ProfileMarks &pm, int first) {
+  moe_gemm_kernel<BITS, FOLDED, true><<<gemm_grid<BITS, FOLDED, true>(max_g1), kThreads, 0, st>>>(a);
+  int rc = check_launch("moe_gemm1");
+  if (rc) return rc;
+  pm.mark(first + 1);
+  moe_gemm_kernel<BITS, FOLDED, false><<<gemm_grid<BITS, FOLDED, false>(max_g2), kThreads, 0, st>>>(a);
+  rc = check_launch("moe_gemm2");
+  if (rc) return rc;
+  pm.mark(first + 2);
+  const int64_t n8 = a.T * a.H / 8;
+  combine_kernel<<<static_cast<int>(ceil_div(n8, kCombineBlock)), kCombineBlock, 0, st>>>(a.ybuf, a.ids, a.T, a.H,
+                                                                                          a.k, a.E, a.out);
+  rc = check_launch("moe_combine");
+  if (rc) return rc;
+  pm.mark(first + 3);
+  return LQ_OK;
+}
+
+// plan -> G1 -> G2 -> combine (x_permuted: the router already wrote the
+// K-slot permuted x into the workspace; otherwise a permute kernel runs first)
+int moe_forward_impl(const void *x, bool x_permuted, int64_t T, int H, int I, int E, int k, const int8_t *q1,
+                     const float *s1, const int8_t *q2, const float *s2, int bits, int64_t group_w1,
+                     int64_t group_w2, int flags, const int32_t *topk_ids, const float *topk_weights, char *ws,
+                     void *out, hipStream_t st, ProfileMarks &pm, int first_mark) {
   const WsLayout w = ws_layout(T, H, I, E, k);
   const int64_t N = T * k;
-  const int mc = unit_rows_for(N, E);
-  const int64_t max_units = max_units_for(N, E, mc);
   const int64_t g1 = effective_group(H, group_w1);
   const int64_t g2 = effective_group(I, group_w2);
+  // the folded form applies one scale per 128-wide K chunk
+  const bool folded = (flags & LQ_MOE_FOLDED_SCALES) && g1 % kKC == 0 && g2 % kKC == 0;
+
+  PlanArgs p;
+  p.ids = topk_ids;
+  p.N = N;
+  p.E = E;
+  p.counts = reinterpret_cast<int32_t *>(ws + w.counts);
+  p.offsets = reinterpret_cast<int32_t *>(ws + w.offsets);
+  p.sorted = reinterpret_cast<int32_t *>(ws + w.sorted);
+  p.items = reinterpret_cast<uint2 *>(ws + w.items);
+  p.hdr = reinterpret_cast<PlanHeader *>(ws + w.hdr);
+  p.nf = I / kF1;
+  p.nr = H / kR2;
+  uint16_t *xperm = reinterpret_cast<uint16_t *>(ws + w.xperm);
+  if (!x_permuted) {
+    const int64_t n8 = T * H / 8;
+    permute_rows_kernel<<<static_cast<int>(ceil_div(n8, 256)), 256, 0, st>>>(static_cast<const uint16_t *>(x), n8,
+                                                                             xperm);
+  }
+  plan_kernel<<<1, kPlanBlock, 0, st>>>(p);
+  int rc = check_launch("moe_plan");
+  if (rc) return rc;
+  pm.mark(first_mark);
 
   MoeArgs a;
-  a.x = static_cast<const uint16_t *>(x);
+  a.xperm = xperm;
   a.q1 = q1;
   a.s1 = s1;
   a.q2 = q2;
   a.s2 = s2;
   a.ids = topk_ids;
   a.topk_w = topk_weights;
-  a.sorted = reinterpret_cast<const int32_t *>(ws + w.sorted);
-  a.units = reinterpret_cast<const int32_t *>(ws + w.units);
-  a.n_units = reinterpret_cast<const int32_t *>(ws + w.n_units);
+  a.offsets = p.offsets;
+  a.sorted = p.sorted;
+  a.items = p.items;
+  a.hdr = p.hdr;
   a.act = reinterpret_cast<uint16_t *>(ws + w.act);
   a.ybuf = reinterpret_cast<float *>(ws + w.ybuf);
   a.out = static_cast<uint16_t *>(out);
@@ -455,35 +852,15 @@ int moe_forward_impl(const void *x, int64_t T, int H, int I, int E, int k, const
   a.ng1 = static_cast<int>(H / g1);
   a.g2 = static_cast<int>(g2);
   a.ng2 = static_cast<int>(I / g2);
-
-  int rc = launch_permute(topk_ids, N, E, reinterpret_cast<int32_t *>(ws + w.counts),
-                          reinterpret_cast<int32_t *>(ws + w.offsets), reinterpret_cast<int32_t *>(ws + w.sorted),
-                          mc, reinterpret_cast<int32_t *>(ws + w.units), reinterpret_cast<int32_t *>(ws + w.n_units),
-                          st);
+  const int64_t blocks = std::min<int64_t>(E, N) + N / kRowsMax;
+  const int64_t max_g1 = blocks * (I / kF1), max_g2 = blocks * (H / kR2);
+  if (bits == 4)
+    rc = folded ? launch_phases<4, true>(a, max_g1, max_g2, st, pm, first_mark)
+                : launch_phases<4, false>(a, max_g1, max_g2, st, pm, first_mark);
+  else
+    rc = folded ? launch_phases<8, true>(a, max_g1, max_g2, st, pm, first_mark)
+                : launch_phases<8, false>(a, max_g1, max_g2, st, pm, first_mark);
   if (rc) return rc;
-  pm.mark(first_mark);
-#define LQ_GEMM(WHICH)                                       \
-  if (bits == 4) {                                           \
-    if (mc == 16) WHICH<4, 1>(a, max_units, st);             \
-    else if (mc == 32) WHICH<4, 2>(a, max_units, st);        \
-    else WHICH<4, 4>(a, max_units, st);                      \
-  } else {                                                   \
-    if (mc == 16) WHICH<8, 1>(a, max_units, st);             \
-    else if (mc == 32) WHICH<8, 2>(a, max_units, st);        \
-    else WHICH<8, 4>(a, max_units, st);                      \
-  }
-  LQ_GEMM(launch_gemm1);
-  pm.mark(first_mark + 1);
-  LQ_GEMM(launch_gemm2);
-#undef LQ_GEMM
-  rc = check_launch("moe_gemm");
-  if (rc) return rc;
-  pm.mark(first_mark + 2);
-  const int64_t nthreads = T * (H >> 2);
-  combine_kernel<<<static_cast<int>(ceil_div(nthreads, 256)), 256, 0, st>>>(a.ybuf, topk_ids, T, H, k, E, a.out);
-  rc = check_launch("moe_combine");
-  if (rc) return rc;
-  pm.mark(first_mark + 3);
   return pm.rc;
 }
 
@@ -495,6 +872,20 @@ ProfileMarks take_profile(hipStream_t st) {
 }
 
 }  // namespace
+
+int launch_permute(const int32_t *ids, int64_t N, int E, int32_t *counts, int32_t *offsets, int32_t *sorted,
+                   hipStream_t st) {
+  PlanArgs p{};
+  p.ids = ids;
+  p.N = N;
+  p.E = E;
+  p.counts = counts;
+  p.offsets = offsets;
+  p.sorted = sorted;
+  p.items = nullptr;
+  plan_kernel<<<1, kPlanBlock, 0, st>>>(p);
+  return check_launch("moe_permute");
+}
 
 }  // namespace lq
 
@@ -514,25 +905,28 @@ extern "C" int lq_moe_profile_events(void *const *events, int n_events) {
 
 extern "C" int lq_moe_forward(const void *x, int64_t T, int H, int I, int E, int k, const int8_t *q1,
                               const float *s1, const int8_t *q2, const float *s2, int bits, int64_t group_w1,
-                              int64_t group_w2, const int32_t *topk_ids, const float *topk_weights,
+                              int64_t group_w2, int flags, const int32_t *topk_ids, const float *topk_weights,
                               void *workspace, size_t ws_bytes, void *out, lq_stream_t stream) {
   const hipStream_t st = as_stream(stream);
   ProfileMarks pm = take_profile(st);
-  int rc = validate_layer(x, T, H, I, E, k, q1, s1, q2, s2, bits, group_w1, group_w2, workspace, ws_bytes, out);
+  int rc = validate_layer(x, T, H, I, E, k, q1, s1, q2, s2, bits, group_w1, group_w2, flags, workspace, ws_bytes,
+                          out);
   if (rc || T == 0) return rc;
   if (!topk_ids || !topk_weights) return fail(LQ_ERR_VALUE, "moe_forward: null routing pointer");
   pm.mark(0);
-  return moe_forward_impl(x, T, H, I, E, k, q1, s1, q2, s2, bits, group_w1, group_w2, topk_ids, topk_weights,
-                          static_cast<char *>(workspace), out, st, pm, 1);
+  return moe_forward_impl(x, false, T, H, I, E, k, q1, s1, q2, s2, bits, group_w1, group_w2, flags, topk_ids,
+                          topk_weights, static_cast<char *>(workspace), out, st, pm, 1);
 }
 
 extern "C" int lq_moe_layer(const void *x, const void *logits, int logits_dtype, int64_t T, int H, int I, int E,
                             int k, int renormalize, const int8_t *q1, const float *s1, const int8_t *q2,
-                            const float *s2, int bits, int64_t group_w1, int64_t group_w2, void *workspace,
-                            size_t ws_bytes, void *out, int32_t *topk_ids_out, lq_stream_t stream) {
+                            const float *s2, int bits, int64_t group_w1, int64_t group_w2, int flags,
+                            void *workspace, size_t ws_bytes, void *out, int32_t *topk_ids_out,
+                            lq_stream_t stream) {
   const hipStream_t st = as_stream(stream);
   ProfileMarks pm = take_profile(st);
-  int rc = validate_layer(x, T, H, I, E, k, q1, s1, q2, s2, bits, group_w1, group_w2, workspace, ws_bytes, out);
+  int rc = validate_layer(x, T, H, I, E, k, q1, s1, q2, s2, bits, group_w1, group_w2, flags, workspace, ws_bytes,
+                          out);
   if (rc || T == 0) return rc;
   if (!logits) return fail(LQ_ERR_VALUE, "moe_layer: null logits");
   char *ws = static_cast<char *>(workspace);
@@ -540,9 +934,11 @@ extern "C" int lq_moe_layer(const void *x, const void *logits, int logits_dtype,
   int32_t *ids = topk_ids_out ? topk_ids_out : reinterpret_cast<int32_t *>(ws + w.ids);
   float *weights = reinterpret_cast<float *>(ws + w.weights);
   pm.mark(0);
-  rc = launch_route_topk(logits, logits_dtype, T, E, k, renormalize, ids, weights, st);
+  // the router also writes the K-slot permuted copy of x the layer stages from
+  rc = launch_route_topk(logits, logits_dtype, T, E, k, renormalize, ids, weights, st,
+                         static_cast<const uint16_t *>(x), H, reinterpret_cast<uint16_t *>(ws + w.xperm));
   if (rc) return rc;
   pm.mark(1);
-  return moe_forward_impl(x, T, H, I, E, k, q1, s1, q2, s2, bits, group_w1, group_w2, ids, weights, ws, out, st,
-                          pm, 2);
+  return moe_forward_impl(x, true, T, H, I, E, k, q1, s1, q2, s2, bits, group_w1, group_w2, flags, ids, weights, ws,
+                          out, st, pm, 2);
 }

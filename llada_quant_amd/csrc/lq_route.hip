@@ -1,5 +1,6 @@
-// lq_route.hip -- routing front end for gfx950: top-k softmax router and the
-// stable expert permutation of the T*k assignments.
+// lq_route.hip -- routing front end for gfx950: top-k softmax router, the
+// gathered top-k weights, and the entry point of the stable expert
+// permutation of the T*k assignments (its kernel is lq_moe.hip's plan).
 //
 // Routing restates TritonFusedMoEBlock.forward as trajectory/llada.py:228-234
 // records it: softmax(logits, dim=-1, dtype=float32).topk(k).indices.
@@ -15,24 +16,33 @@ namespace {
 constexpr int kRouteBlock = 256;  // 4 tokens per block, one wave each
 
 // One wavefront per token; lane l holds experts l, l+64, ... (EPL of them).
-// ids are chosen by descending logit with ties to the lower expert id (the
-// order of descending probability: softmax is monotone).  Weights are the
-// fp32 softmax probabilities of the chosen experts.
+// Each expert's rank is counted directly: rank(e) = #{e' : x[e'] > x[e], or
+// x[e'] == x[e] and e' < e} over the token's logits (read back from LDS), so
+// ids come out in descending-logit order with ties to the lower expert id --
+// the order of descending probability, softmax being monotone -- with no
+// serial selection rounds.  Experts of rank < k write their id and fp32
+// softmax probability to slot `rank`.  With xperm != nullptr the wave also
+// copies its token's row of x into xperm in the MoE kernel's K-slot order.
 template <int LDT, int EPL>
 __global__ __launch_bounds__(kRouteBlock) void route_topk_kernel(const void *__restrict__ logits, int64_t T,
                                                                  int E, int k, int renorm,
                                                                  int32_t *__restrict__ ids,
-                                                                 float *__restrict__ weights) {
+                                                                 float *__restrict__ weights,
+                                                                 const uint16_t *__restrict__ x, int H,
+                                                                 uint16_t *__restrict__ xperm) {
+  __shared__ float row[kRouteBlock / 64][kMaxExperts];
   const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
   const int64_t t = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
-  if (t >= T) return;  // uniform per wave
-  float x[EPL];
+  if (t >= T) return;  // uniform per wave; no block-wide barrier below
+  float v[EPL];
   float m = -__builtin_inff();
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
     const int e = lane + 64 * j;
-    x[j] = e < E ? load_f32<LDT>(logits, t * E + e) : -__builtin_inff();
-    m = fmaxf(m, x[j]);
+    v[j] = e < E ? load_f32<LDT>(logits, t * E + e) : -__builtin_inff();
+    if (e < E) row[wave][e] = v[j];
+    m = fmaxf(m, v[j]);
   }
   m = wave_max(m);
   float p[EPL];
@@ -40,53 +50,43 @@ __global__ __launch_bounds__(kRouteBlock) void route_topk_kernel(const void *__r
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
     const int e = lane + 64 * j;
-    p[j] = e < E ? expf(x[j] - m) : 0.0f;
+    p[j] = e < E ? expf(v[j] - m) : 0.0f;
     s += p[j];
   }
   s = wave_sum(s);
+  int rank[EPL];
 #pragma unroll
-  for (int j = 0; j < EPL; ++j) p[j] = p[j] / s;
-
-  uint32_t taken = 0;  // bit j: slot j of this lane already chosen
-  float wsum = 0.0f;
-  for (int r = 0; r < k; ++r) {
-    float bv = -__builtin_inff();
-    int bi = 0x7FFFFFFF;
+  for (int j = 0; j < EPL; ++j) rank[j] = 0;
+  // the wave's LDS row is written and read by this wave only (lockstep)
+  __builtin_amdgcn_wave_barrier();
+  for (int c = 0; c < E; ++c) {
+    const float xc = row[wave][c];
 #pragma unroll
     for (int j = 0; j < EPL; ++j) {
       const int e = lane + 64 * j;
-      if (e < E && !((taken >> j) & 1u) && (x[j] > bv || (x[j] == bv && e < bi))) {
-        bv = x[j];
-        bi = e;
-      }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, 64);
-      const int oi = __shfl_xor(bi, o, 64);
-      if (ov > bv || (ov == bv && oi < bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    // every lane now holds the winner bi; its owner marks it taken
-    float pw = 0.0f;
-#pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-      if (lane + 64 * j == bi) {
-        taken |= 1u << j;
-        pw = p[j];
-      }
-    }
-    pw = __shfl(pw, bi & 63, 64);
-    wsum += pw;
-    if (lane == 0) {
-      ids[t * k + r] = bi;
-      weights[t * k + r] = pw;
+      rank[j] += (xc > v[j] || (xc == v[j] && c < e)) ? 1 : 0;
     }
   }
-  if (renorm && lane == 0) {
-    for (int r = 0; r < k; ++r) weights[t * k + r] = weights[t * k + r] / wsum;
+  float wsel = 0.0f;
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int e = lane + 64 * j;
+    if (e < E && rank[j] < k) wsel += p[j] / s;
+  }
+  const float wsum = renorm ? wave_sum(wsel) : 1.0f;
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int e = lane + 64 * j;
+    if (e < E && rank[j] < k) {
+      const float pw = p[j] / s;
+      ids[t * k + rank[j]] = e;
+      weights[t * k + rank[j]] = renorm ? pw / wsum : pw;
+    }
+  }
+  if (xperm != nullptr) {
+    const uint4 *src = reinterpret_cast<const uint4 *>(x + t * H);
+    uint4 *dst = reinterpret_cast<uint4 *>(xperm + t * H);
+    for (int c = lane; c < (H >> 3); c += 64) dst[c] = permute_kslots(src[c]);
   }
 }
 
@@ -108,137 +108,7 @@ __global__ void gather_weights_kernel(const float *__restrict__ probs, const IdT
     for (int j = 0; j < k; ++j) weights[t * k + j] = weights[t * k + j] / s;
 }
 
-constexpr int kPermBlock = 1024;
-constexpr int kPermWaves = kPermBlock / 64;
-
-// exclusive scan of v over the E (<= kMaxExperts) entries, by wave 0; lane l
-// owns entries 4l..4l+3.  Returns the total through *total.
-__device__ void wave0_exclusive_scan(const int *in, int *out, int E, int *total) {
-  const int lane = threadIdx.x & 63;
-  int v[4];
-  int local = 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = 4 * lane + i;
-    v[i] = e < E ? in[e] : 0;
-    local += v[i];
-  }
-  int incl = local;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(incl, o, 64);
-    if (lane >= o) incl += y;
-  }
-  int run = incl - local;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = 4 * lane + i;
-    if (e < E) out[e] = run;
-    run += v[i];
-  }
-  const int tot = __shfl(incl, 63, 64);
-  if (lane == 0) *total = tot;
-}
-
-// Single-block stable counting sort of the N = T*k assignments.
-// Optionally (unit_rows > 0) also emits the GEMM work units: each expert's
-// sorted run split into chunks of unit_rows rows, as (expert, first sorted
-// position, rows) triples, expert-major; n_units receives their count.
-__global__ __launch_bounds__(kPermBlock) void permute_kernel(const int32_t *__restrict__ ids, int64_t N, int E,
-                                                             int32_t *__restrict__ counts,
-                                                             int32_t *__restrict__ offsets,
-                                                             int32_t *__restrict__ sorted, int unit_rows,
-                                                             int32_t *__restrict__ units,
-                                                             int32_t *__restrict__ n_units) {
-  __shared__ int hist[kMaxExperts];
-  __shared__ int base[kMaxExperts];
-  __shared__ int ustart[kMaxExperts];
-  __shared__ int wcnt[kPermWaves][kMaxExperts];
-  __shared__ int total;
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
-  for (int e = tid; e < kMaxExperts; e += kPermBlock) hist[e] = 0;
-  for (int i = tid; i < kPermWaves * kMaxExperts; i += kPermBlock) (&wcnt[0][0])[i] = 0;
-  __syncthreads();
-  for (int64_t a = tid; a < N; a += kPermBlock) {
-    const int id = ids[a];
-    if (id >= 0 && id < E) atomicAdd(&hist[id], 1);
-  }
-  __syncthreads();
-  if (wave == 0) wave0_exclusive_scan(hist, base, E, &total);
-  __syncthreads();
-  for (int e = tid; e < E; e += kPermBlock) {
-    counts[e] = hist[e];
-    offsets[e] = base[e];
-  }
-  if (tid == 0) offsets[E] = total;
-  if (unit_rows > 0) {
-    // per-expert unit counts, then their exclusive scan
-    __syncthreads();
-    for (int e = tid; e < E; e += kPermBlock) wcnt[0][e] = (hist[e] + unit_rows - 1) / unit_rows;
-    __syncthreads();
-    if (wave == 0) wave0_exclusive_scan(wcnt[0], ustart, E, n_units);
-    __syncthreads();
-    for (int e = tid; e < E; e += kPermBlock) {
-      const int nu = wcnt[0][e];
-      for (int u = 0; u < nu; ++u) {
-        const int row0 = base[e] + u * unit_rows;
-        const int rows = min(unit_rows, hist[e] - u * unit_rows);
-        int32_t *dst = units + 3 * (ustart[e] + u);
-        dst[0] = e;
-        dst[1] = row0;
-        dst[2] = rows;
-      }
-    }
-    __syncthreads();
-    for (int e = tid; e < E; e += kPermBlock) wcnt[0][e] = 0;
-  }
-  __syncthreads();
-
-  // key bits: experts are < E <= 256, invalid lanes use key E
-  int nbits = 1;
-  while ((1 << nbits) <= E) ++nbits;
-  const unsigned long long lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int64_t chunk = 0; chunk < N; chunk += kPermBlock) {
-    const int64_t a = chunk + tid;
-    const int raw = a < N ? ids[a] : -1;
-    const bool valid = raw >= 0 && raw < E;
-    const int key = valid ? raw : E;
-    unsigned long long peers = ~0ull;
-    for (int b = 0; b < nbits; ++b) {
-      const bool bit = (key >> b) & 1;
-      const unsigned long long bal = __ballot(bit);
-      peers &= bit ? bal : ~bal;
-    }
-    const int rank = __popcll(peers & lt_mask);
-    if (valid && rank == 0) wcnt[wave][key] = __popcll(peers);
-    __syncthreads();
-    if (valid) {
-      int pos = base[key] + rank;
-      for (int w = 0; w < wave; ++w) pos += wcnt[w][key];
-      sorted[pos] = static_cast<int32_t>(a);
-    }
-    __syncthreads();
-    for (int e = tid; e < E; e += kPermBlock) {
-      int s = 0;
-      for (int w = 0; w < kPermWaves; ++w) {
-        s += wcnt[w][e];
-        wcnt[w][e] = 0;
-      }
-      base[e] += s;
-    }
-    __syncthreads();
-  }
-}
-
 }  // namespace
-
-int launch_permute(const int32_t *ids, int64_t N, int E, int32_t *counts, int32_t *offsets, int32_t *sorted,
-                   int unit_rows, int32_t *units, int32_t *n_units, hipStream_t st) {
-  permute_kernel<<<1, kPermBlock, 0, st>>>(ids, N, E, counts, offsets, sorted, unit_rows, units, n_units);
-  return check_launch("moe_permute");
-}
 
 }  // namespace lq
 
@@ -246,7 +116,8 @@ using namespace lq;
 
 namespace lq {
 int launch_route_topk(const void *logits, int logits_dtype, int64_t T, int E, int k, int renormalize,
-                      int32_t *topk_ids, float *topk_weights, hipStream_t st) {
+                      int32_t *topk_ids, float *topk_weights, hipStream_t st, const uint16_t *x, int H,
+                      uint16_t *xperm) {
   if (logits_dtype != LQ_F32 && logits_dtype != LQ_BF16 && logits_dtype != LQ_F16)
     return fail(LQ_ERR_VALUE, "route_topk: logits must be float32, float16 or bfloat16");
   if (E < 1 || E > kMaxExperts)
@@ -260,7 +131,7 @@ int launch_route_topk(const void *logits, int logits_dtype, int64_t T, int E, in
 #define LQ_ROUTE_LAUNCH(EPL)                                                                         \
   LQ_DISPATCH_DTYPE(logits_dtype, LDT, {                                                             \
     route_topk_kernel<LDT, EPL><<<static_cast<int>(blocks), kRouteBlock, 0, st>>>(                   \
-        logits, T, E, k, renormalize, topk_ids, topk_weights);                                       \
+        logits, T, E, k, renormalize, topk_ids, topk_weights, x, H, xperm);                          \
   })
   if (E <= 64) {
     LQ_ROUTE_LAUNCH(1);
@@ -303,5 +174,5 @@ extern "C" int lq_moe_permute(const int32_t *topk_ids, int64_t T, int k, int E, 
   if (T < 0 || k < 1) return fail(LQ_ERR_VALUE, "moe_permute: bad shape");
   if (T * k > 0x7FFFFFFF) return fail(LQ_ERR_UNSUPPORTED, "moe_permute: too many assignments");
   if (!counts || !offsets || (T > 0 && (!topk_ids || !sorted))) return fail(LQ_ERR_VALUE, "moe_permute: null pointer");
-  return launch_permute(topk_ids, T * k, E, counts, offsets, sorted, 0, nullptr, nullptr, as_stream(stream));
+  return launch_permute(topk_ids, T * k, E, counts, offsets, sorted, as_stream(stream));
 }

@@ -22,7 +22,8 @@ LIB_PATH = os.path.join(_PKG_DIR, "liblladaq.so")
 LQ_OK, LQ_ERR_VALUE, LQ_ERR_UNSUPPORTED, LQ_ERR_RUNTIME = 0, 1, 2, 3
 LQ_F32, LQ_F16, LQ_BF16 = 0, 1, 2
 LQ_SCALE_AMAX, LQ_SCALE_MSE = 0, 1
-ABI_VERSION = 1
+ABI_VERSION = 2
+LQ_MOE_FOLDED_SCALES = 1
 
 DTYPE_CODES = {torch.float32: LQ_F32, torch.float16: LQ_F16, torch.bfloat16: LQ_BF16}
 
@@ -41,10 +42,10 @@ SIGNATURES = {
     "lq_gather_topk_weights": (_I32, [_P, _P, _I32, _I64, _I32, _I32, _I32, _P, _P, _P]),
     "lq_moe_permute": (_I32, [_P, _I64, _I32, _I32, _P, _P, _P, _P]),
     "lq_moe_workspace_bytes": (_SZ, [_I64, _I32, _I32, _I32, _I32]),
-    "lq_moe_forward": (_I32, [_P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _I32, _I64, _I64, _P, _P, _P,
-                              _SZ, _P, _P]),
+    "lq_moe_forward": (_I32, [_P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _I32, _I64, _I64, _I32, _P, _P,
+                              _P, _SZ, _P, _P]),
     "lq_moe_layer": (_I32, [_P, _P, _I32, _I64, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _I32, _I64, _I64,
-                            _P, _SZ, _P, _P, _P]),
+                            _I32, _P, _SZ, _P, _P, _P]),
     "lq_moe_profile_events": (_I32, [_P, _I32]),
 }
 

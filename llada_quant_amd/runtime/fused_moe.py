@@ -54,8 +54,16 @@ def fused_moe_packed(
     topk_weights: torch.Tensor,
     out: Optional[torch.Tensor] = None,
     workspace: Optional[torch.Tensor] = None,
+    folded_scales: bool = False,
 ) -> torch.Tensor:
-    """The layer on explicit operands: ``x [T, H]`` bf16, int32 ids and fp32 weights ``[T, k]``."""
+    """The layer on explicit operands: ``x [T, H]`` bf16, int32 ids and fp32 weights ``[T, k]``.
+
+    The matrix cores consume the reference's dequantized BF16 weights
+    ``bf16(fp32(q) * s)`` bit for bit.  ``folded_scales`` instead feeds the
+    codes as exact integers and multiplies each group's fp32 scale into their
+    dot product: cheaper, but without the per-weight BF16 rounding the output
+    moves by about the reference tolerance (mean-relative ~5e-3).
+    """
     g1, g2, I = _check_weights(x, w1, w2)
     T, H = x.shape
     E = w1.logical_shape[0]
@@ -77,11 +85,15 @@ def fused_moe_packed(
         with torch.cuda.device(device):
             rc = lib.lq_moe_forward(
                 _lib.ptr(xc), T, H, I, E, k, _lib.ptr(q1), _lib.ptr(s1), _lib.ptr(q2), _lib.ptr(s2), w1.bits, g1, g2,
-                _lib.ptr(ids), _lib.ptr(wts), _lib.ptr(workspace), workspace.numel(), _lib.ptr(out),
-                _lib.stream(device),
+                _moe_flags(folded_scales), _lib.ptr(ids), _lib.ptr(wts), _lib.ptr(workspace), workspace.numel(),
+                _lib.ptr(out), _lib.stream(device),
             )
         _lib.check(rc, "fused_moe")
     return out
+
+
+def _moe_flags(folded_scales: bool) -> int:
+    return _lib.LQ_MOE_FOLDED_SCALES if folded_scales else 0
 
 
 def _check_weights(x: torch.Tensor, w1: QuantResult, w2: QuantResult):
@@ -134,6 +146,7 @@ def fused_moe(
     *,
     renormalize: bool = False,
     topk_weights: Optional[torch.Tensor] = None,
+    folded_scales: bool = False,
 ) -> torch.Tensor:
     """Quantized MoE layer output ``[..., H]`` (bf16) for ``hidden_states [..., H]``.
 
@@ -154,7 +167,7 @@ def fused_moe(
         ids, weights = gather_topk_weights(gating_output.reshape(x.shape[0], -1), topk_ids, renormalize)
     else:
         ids, weights = topk_ids, topk_weights
-    out = fused_moe_packed(x, q1, q2, ids, weights)
+    out = fused_moe_packed(x, q1, q2, ids, weights, folded_scales=folded_scales)
     return out.reshape(hidden_states.shape)
 
 
@@ -165,6 +178,7 @@ def moe_layer(
     w2: PackedWeight,
     top_k: int,
     renormalize: bool = False,
+    folded_scales: bool = False,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """Router + quantized experts in one library call: ``(output [..., H], topk_ids [T, k] int32)``.
 
@@ -200,7 +214,7 @@ def moe_layer(
             rc = lib.lq_moe_layer(
                 _lib.ptr(xc), _lib.ptr(logits), _lib.dtype_code(logits.dtype, "router_logits"), T, H, I, E, top_k,
                 int(renormalize), _lib.ptr(q1c), _lib.ptr(s1), _lib.ptr(q2c), _lib.ptr(s2), q1.bits, g1, g2,
-                _lib.ptr(workspace), workspace.numel(), _lib.ptr(out), _lib.ptr(ids), _lib.stream(device),
+                _moe_flags(folded_scales), _lib.ptr(workspace), workspace.numel(), _lib.ptr(out), _lib.ptr(ids), _lib.stream(device),
             )
         _lib.check(rc, "moe_layer")
     return out.reshape(hidden_states.shape), ids

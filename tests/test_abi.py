@@ -119,10 +119,10 @@ def test_moe_workspace_size_is_monotone_in_tokens_and_covers_the_buffers():
 def test_moe_forward_rejects_unsupported_shapes_on_the_host():
     lib = _lib.load()
     ws = lib.lq_moe_workspace_bytes(8, 100, 64, 4, 2)
-    rc, msg = _rc_and_msg(lib.lq_moe_forward(NULL, 8, 100, 64, 4, 2, NULL, NULL, NULL, NULL, 4, 128, 128, NULL,
+    rc, msg = _rc_and_msg(lib.lq_moe_forward(NULL, 8, 100, 64, 4, 2, NULL, NULL, NULL, NULL, 4, 128, 128, 0, NULL,
                                              NULL, NULL, ws, NULL, NULL))
     assert rc == _lib.LQ_ERR_UNSUPPORTED and "hidden" in msg
-    rc, msg = _rc_and_msg(lib.lq_moe_forward(NULL, 8, 128, 64, 4, 5, NULL, NULL, NULL, NULL, 4, 128, 128, NULL,
+    rc, msg = _rc_and_msg(lib.lq_moe_forward(NULL, 8, 128, 64, 4, 5, NULL, NULL, NULL, NULL, 4, 128, 128, 0, NULL,
                                              NULL, NULL, ws, NULL, NULL))
     assert rc == _lib.LQ_ERR_VALUE and "top_k" in msg
 

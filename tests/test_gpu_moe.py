@@ -19,7 +19,7 @@ import torch
 
 from conftest import bits_u16
 from llada_quant_amd.algorithms.symmetric import quantize_tensor
-from llada_quant_amd.runtime.fused_moe import fused_moe, fused_moe_packed, moe_layer
+from llada_quant_amd.runtime.fused_moe import fused_moe, fused_moe_packed, moe_layer, workspace_bytes
 from llada_quant_amd.runtime.routing import route_topk
 from oracle import oracle as O
 from test_gpu_route import zipf_logits
@@ -49,14 +49,25 @@ def oracle_out(x, q1, q2, ids, weights, rows=None):
     return O.moe_forward(bits_u16(xs), d1, d2, ids_np, w_np)
 
 
-def assert_close(out: torch.Tensor, ref: np.ndarray):
+def assert_close(out: torch.Tensor, ref: np.ndarray, mean_rel_bar: float = MEAN_REL):
     o = out.float().cpu().numpy().astype(np.float64)
     r = ref.astype(np.float64)
     max_abs = np.abs(o - r).max()
     mean_rel = np.abs(o - r).sum() / np.abs(r).sum()
     assert max_abs < MAX_ABS, f"max abs error {max_abs:.3e}"
-    assert mean_rel < MEAN_REL, f"mean relative error {mean_rel:.3e}"
+    assert mean_rel < mean_rel_bar, f"mean relative error {mean_rel:.3e}"
     return max_abs, mean_rel
+
+
+# The folded form skips the per-weight bf16 rounding of the reference, which
+# moves the output by about the north-star bar itself (a float64 simulation of
+# both forms against the oracle gives mean-relative 4.6e-3 .. 5.1e-3 for the
+# folded form and 1.4e-3 for the exact one); it is held to 1e-2.
+FOLDED_MEAN_REL = 1e-2
+
+
+def bar(folded):
+    return FOLDED_MEAN_REL if folded else MEAN_REL
 
 
 @pytest.mark.parametrize("bits", [4, 8])
@@ -71,30 +82,33 @@ def test_tiny_reference_shape(dev, bits, T, k):
     assert_close(out, oracle_out(x, q1, q2, ids, w))
 
 
-def test_c1_plumbing_case(dev):
+@pytest.mark.parametrize("folded", [False, True])
+def test_c1_plumbing_case(dev, folded):
     """C1: E=16, H=1024, I=512, INT4 G=128, 256 tokens, top-2 renormalized; both layers."""
     g = torch.Generator().manual_seed(1)
     x = torch.randn(256, 1024, generator=g).to(torch.bfloat16).to(dev)
     for layer in range(2):
         q1, q2 = make_layer(dev, 16, 1024, 512, 4, seed=10 + layer)
         ids, w = route_topk(torch.randn(256, 16, generator=g).to(dev), 2, renormalize=True)
-        out = fused_moe_packed(x, q1, q2, ids, w)
-        assert_close(out, oracle_out(x, q1, q2, ids, w))
+        out = fused_moe_packed(x, q1, q2, ids, w, folded_scales=folded)
+        assert_close(out, oracle_out(x, q1, q2, ids, w), bar(folded))
         x = out
 
 
-def test_c2_int8_sampled(dev):
+@pytest.mark.parametrize("folded", [False, True])
+def test_c2_int8_sampled(dev, folded):
     """C2: INT8, E=64, H=2048, I=1024, 512 tokens, top-8 (oracle on 96 sampled tokens)."""
     q1, q2 = make_layer(dev, 64, 2048, 1024, 8, seed=2)
     g = torch.Generator().manual_seed(2)
     x = torch.randn(512, 2048, generator=g).to(torch.bfloat16).to(dev)
     ids, w = route_topk(torch.randn(512, 64, generator=g).to(dev), 8)
-    out = fused_moe_packed(x, q1, q2, ids, w)
+    out = fused_moe_packed(x, q1, q2, ids, w, folded_scales=folded)
     rows = np.sort(np.random.default_rng(2).choice(512, 96, replace=False))
-    assert_close(out[torch.from_numpy(rows).to(dev)], oracle_out(x, q1, q2, ids, w, rows))
+    assert_close(out[torch.from_numpy(rows).to(dev)], oracle_out(x, q1, q2, ids, w, rows), bar(folded))
 
 
-def test_c4_zipf_skew_full(dev):
+@pytest.mark.parametrize("folded", [False, True])
+def test_c4_zipf_skew_full(dev, folded):
     """C4: INT4 MSE, 64 tokens, top-8, Zipf(1.1)-skewed routing (empty and hot experts)."""
     q1, q2 = make_layer(dev, 64, 2048, 1024, 4, seed=4, search="mse", grid=16)
     g = torch.Generator().manual_seed(4)
@@ -102,19 +116,22 @@ def test_c4_zipf_skew_full(dev):
     ids, w = route_topk(zipf_logits(64, 64, seed=4).to(dev), 8)
     counts = torch.bincount(ids.reshape(-1).long().cpu(), minlength=64)
     assert (counts == 0).any() and counts.max() > 16  # the skew really is there
-    out = fused_moe_packed(x, q1, q2, ids, w)
-    assert_close(out, oracle_out(x, q1, q2, ids, w))
+    ws = torch.empty(workspace_bytes(64, 2048, 1024, 64, 8), dtype=torch.uint8, device=dev)
+    out = fused_moe_packed(x, q1, q2, ids, w, workspace=ws, folded_scales=folded)
+    assert_close(out, oracle_out(x, q1, q2, ids, w), bar(folded))
 
 
-def test_c3_large_token_count_sampled(dev):
+@pytest.mark.parametrize("folded", [False, True])
+def test_c3_large_token_count_sampled(dev, folded):
     """C3: INT4, 4096 tokens, top-8 (~512 rows per expert), oracle on 48 sampled tokens."""
     q1, q2 = make_layer(dev, 64, 2048, 1024, 4, seed=3)
     g = torch.Generator().manual_seed(3)
     x = torch.randn(4096, 2048, generator=g).to(torch.bfloat16).to(dev)
     ids, w = route_topk(torch.randn(4096, 64, generator=g).to(dev), 8)
-    out = fused_moe_packed(x, q1, q2, ids, w)
+    ws = torch.empty(workspace_bytes(4096, 2048, 1024, 64, 8), dtype=torch.uint8, device=dev)
+    out = fused_moe_packed(x, q1, q2, ids, w, workspace=ws, folded_scales=folded)
     rows = np.sort(np.random.default_rng(3).choice(4096, 48, replace=False))
-    assert_close(out[torch.from_numpy(rows).to(dev)], oracle_out(x, q1, q2, ids, w, rows))
+    assert_close(out[torch.from_numpy(rows).to(dev)], oracle_out(x, q1, q2, ids, w, rows), bar(folded))
 
 
 def test_all_tokens_on_one_expert(dev):
@@ -126,6 +143,23 @@ def test_all_tokens_on_one_expert(dev):
     w = torch.rand(T, 1, device=dev)
     out = fused_moe_packed(x, q1, q2, ids, w)
     assert_close(out, oracle_out(x, q1, q2, ids, w))
+
+
+def test_invalid_and_repeated_ids(dev):
+    """ids outside [0, E) contribute nothing; a token may list one expert twice (fused_moe callers)."""
+    E, H, I, T, k = 8, 256, 128, 40, 3
+    q1, q2 = make_layer(dev, E, H, I, 4, seed=8)
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    ids = torch.randint(0, E, (T, k), generator=g, dtype=torch.int32)
+    ids[::5, 1] = -1
+    ids[::7, 2] = E
+    ids[::3, 0] = ids[::3, 2].clamp(max=E - 1)
+    w = torch.rand(T, k, generator=g)
+    out = fused_moe_packed(x, q1, q2, ids.to(dev), w.to(dev))
+    valid = (ids >= 0) & (ids < E)
+    ref = oracle_out(x, q1, q2, torch.where(valid, ids, torch.zeros_like(ids)), torch.where(valid, w, 0.0))
+    assert_close(out, ref)
 
 
 def test_output_is_deterministic(dev):

@@ -11,7 +11,8 @@ The layer is built so that every product and sum inside the kernel is exact:
   and scales over many binades: y[t, h] = a * W2[h, n(t)], exact in fp32.
 
 So out[t, h] = bf16(a * deq(W2)[h, n(t)]) exactly, with deq the standalone
-(software-rounded) dequant kernel.  A wrong K pairing in either GEMM, a wrong
+(software-rounded) dequant kernel: the matrix cores consume the reference's
+bf16(fp32(q) * s) weights.  A wrong K pairing in either GEMM, a wrong
 token row, or an in-register dequant that rounds differently from
 dequantize_tensor changes the output bits.
 """
