@@ -60,7 +60,24 @@ def parse_args():
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--folded", action="store_true",
                    help="time the LQ_MOE_FOLDED_SCALES form (integer codes, fp32 group scale) as the headline")
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                   help="only run a plain device copy of MIB MiB five times (the known-size kernel that scales "
+                        "rocprofv3 FETCH_SIZE / WRITE_SIZE readings into bytes) and exit")
     return p.parse_args()
+
+
+def copy_calibration(mib):
+    """Five launches of torch's device copy of `mib` MiB: reads and writes exactly mib MiB each."""
+    import torch
+
+    n = mib * (1 << 20)
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_per_launch": n, "launches": 5}), flush=True)
 
 
 def zipf_logits(torch, T, E, seed, s=1.1):
@@ -215,6 +232,9 @@ def cpu_baseline(torch, cfg, layers, x, logits, budget_s):
 
 def main():
     args = parse_args()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (got --gpus {args.gpus}, "
