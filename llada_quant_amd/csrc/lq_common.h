@@ -122,6 +122,76 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// ---------------------------------------------------------------------------
+// exact dequantization fp32(q) * s of packed codes (algorithms/symmetric.py:
+// 272-293), shared by the dequant kernel and the MoE GEMMs.
+//
+// A code enters as n = q + 2^(b-1) (nibble ^ 8, byte ^ 0x80) in the low bits
+// of a binary16 half: the half is the subnormal n * 2^-24 (or 16 n * 2^-24),
+// which v_fma_mix_f32 widens exactly.  fma(n 2^-24, s 2^24, -2^(b-1) s) is
+// then (n - 2^(b-1)) s = q s rounded once -- the rounding of the IEEE
+// product fp32(q) * s.  This needs s * 2^24 finite: dq_fast_ok(s) says so
+// (s < 2^103); callers take dq_slow_* otherwise.
+// ---------------------------------------------------------------------------
+struct DqScale {
+  float s24;  // s * 2^24
+  float s20;  // s * 2^20
+  float c;    // -2^(b-1) * s
+};
+
+template <int BITS>
+__device__ __forceinline__ DqScale dq_scale(float s) {
+  return {s * 16777216.0f, s * 1048576.0f, (BITS == 4 ? -8.0f : -128.0f) * s};
+}
+
+__device__ __forceinline__ bool dq_fast_ok(float s) { return s < 0x1p103f; }
+
+__device__ __forceinline__ float half_lo_f32(uint32_t v) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v & 0xFFFFu)));
+}
+__device__ __forceinline__ float half_hi_f32(uint32_t v) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v >> 16)));
+}
+
+// 8 INT4 codes of one dword (element i in nibble i) -> e[i] = fp32(q_i) * s
+__device__ __forceinline__ void dq_int4x8(uint32_t w, const DqScale &d, float (&e)[8]) {
+  const uint32_t v = w ^ 0x88888888u;
+  const uint32_t vs = v >> 8;
+  const uint32_t t0 = v & 0x000F000Fu;   // n0, n4
+  const uint32_t t1 = v & 0x00F000F0u;   // 16 n1, 16 n5
+  const uint32_t t2 = vs & 0x000F000Fu;  // n2, n6
+  const uint32_t t3 = vs & 0x00F000F0u;  // 16 n3, 16 n7
+  e[0] = fmaf(half_lo_f32(t0), d.s24, d.c);
+  e[4] = fmaf(half_hi_f32(t0), d.s24, d.c);
+  e[1] = fmaf(half_lo_f32(t1), d.s20, d.c);
+  e[5] = fmaf(half_hi_f32(t1), d.s20, d.c);
+  e[2] = fmaf(half_lo_f32(t2), d.s24, d.c);
+  e[6] = fmaf(half_hi_f32(t2), d.s24, d.c);
+  e[3] = fmaf(half_lo_f32(t3), d.s20, d.c);
+  e[7] = fmaf(half_hi_f32(t3), d.s20, d.c);
+}
+
+// 4 INT8 codes of one dword (element i in byte i) -> e[i] = fp32(q_i) * s
+__device__ __forceinline__ void dq_int8x4(uint32_t w, const DqScale &d, float (&e)[4]) {
+  const uint32_t v = w ^ 0x80808080u;
+  const uint32_t t0 = v & 0x00FF00FFu;         // n0, n2
+  const uint32_t t1 = (v >> 8) & 0x00FF00FFu;  // n1, n3
+  e[0] = fmaf(half_lo_f32(t0), d.s24, d.c);
+  e[2] = fmaf(half_hi_f32(t0), d.s24, d.c);
+  e[1] = fmaf(half_lo_f32(t1), d.s24, d.c);
+  e[3] = fmaf(half_hi_f32(t1), d.s24, d.c);
+}
+
+// the same products by plain conversion (any finite or non-finite scale)
+__device__ __forceinline__ void dq_slow_int4x8(uint32_t w, float s, float (&e)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) e[i] = static_cast<float>(static_cast<int32_t>(w << (28 - 4 * i)) >> 28) * s;
+}
+__device__ __forceinline__ void dq_slow_int8x4(uint32_t w, float s, float (&e)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) e[i] = static_cast<float>(static_cast<int32_t>(w << (24 - 8 * i)) >> 24) * s;
+}
+
 // 8 consecutive bf16 (dwords = element pairs 01 23 45 67) -> the K-slot order
 // [0,4,1,5,2,6,3,7] of the MoE kernel's MFMA fragments (dwords 04 15 26 37)
 __device__ __forceinline__ uint4 permute_kslots(uint4 v) {

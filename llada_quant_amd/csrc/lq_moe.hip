@@ -69,17 +69,16 @@ constexpr int kF1 = 64;                         // G1 features per item (128 wei
 constexpr int kR2 = 128;                        // G2 output rows per item
 constexpr int kCombineBlock = 256;             // combine: 8 outputs per thread
 
-// weight chunks in flight per compute wave: deeper for the bandwidth-bound
-// single-row-tile blocks, shallower where two row tiles of accumulators are live
-template <int NRT>
+// 128-wide K chunks of weights in flight per wave: 8 KB per wave either way
+// (INT4: 2 tiles x 1 KB per chunk; INT8: 2 tiles x 2 KB)
+template <int BITS>
 constexpr int depth_for() {
-  return NRT == 1 ? 4 : 2;
+  return BITS == 4 ? 4 : 2;
 }
 
 struct alignas(16) PlanHeader {
-  int32_t ticket[2];  // next G1 / G2 item to hand out
-  int32_t n_g1;       // G1 items (items[0 .. n_g1))
-  int32_t n_g2;       // G2 items (items[n_g1 .. n_g1 + n_g2))
+  int32_t n_blk;  // row blocks in the block table
+  int32_t pad[3];
 };
 
 struct MoeArgs {
@@ -92,8 +91,8 @@ struct MoeArgs {
   const float *topk_w;     // [T*k]
   const int32_t *offsets;  // [E+1]
   const int32_t *sorted;   // [T*k] assignment ids by expert
-  const uint2 *items;      // work list
-  PlanHeader *hdr;
+  const int4 *blocks;      // row blocks {expert, first sorted row, rows, 0}
+  const PlanHeader *hdr;
   uint16_t *act;           // [T*k, I] bf16, by sorted row
   float *ybuf;             // [T*k, H] fp32, by assignment
   uint16_t *out;           // [T, H] bf16
@@ -101,11 +100,6 @@ struct MoeArgs {
   int H, I, E, k;
   int g1, ng1, g2, ng2;    // group length and groups per row of w1 / w2
 };
-
-// work item: x = slice << 8 | expert, y = row block
-__device__ __forceinline__ uint2 item_code(uint32_t e, uint32_t slice, uint32_t blk) {
-  return make_uint2((slice << 8) | e, blk);
-}
 
 // ---------------------------------------------------------------------------
 // weights -> MFMA B fragments (8 bf16 in K slot order [0,4,1,5,2,6,3,7])
@@ -126,26 +120,22 @@ __device__ __forceinline__ uint4 b_int4_folded(uint32_t w) {
   return r;
 }
 
-// INT4 exact: bf16_rne(fp32(q) * s), same slot order.  With n = q + 8
-// (nibble ^ 8): fma(n, s, -8s) rounds (n - 8) s once, exactly as fp32(q) * s
-// does; the high nibbles stay in place (16 n) and use s16 = s / 16 (exact).
-// c = -8 s.
-__device__ __forceinline__ uint4 b_int4_exact(uint32_t w, float s, float s16, float c) {
-  const uint32_t v = w ^ 0x88888888u;
-  const uint32_t lo = v & 0x0F0F0F0Fu;  // n of elements 0, 2, 4, 6
-  const uint32_t hi = v & 0xF0F0F0F0u;  // 16 n of elements 1, 3, 5, 7
-  const float e0 = fmaf(static_cast<float>(lo & 0xFF), s, c);
-  const float e2 = fmaf(static_cast<float>((lo >> 8) & 0xFF), s, c);
-  const float e4 = fmaf(static_cast<float>((lo >> 16) & 0xFF), s, c);
-  const float e6 = fmaf(static_cast<float>(lo >> 24), s, c);
-  const float e1 = fmaf(static_cast<float>(hi & 0xFF), s16, c);
-  const float e3 = fmaf(static_cast<float>((hi >> 8) & 0xFF), s16, c);
-  const float e5 = fmaf(static_cast<float>((hi >> 16) & 0xFF), s16, c);
-  const float e7 = fmaf(static_cast<float>(hi >> 24), s16, c);
-  return make_uint4(cvt2(e0, e4), cvt2(e1, e5), cvt2(e2, e6), cvt2(e3, e7));
+// weights of one lane's 8 K slots -> B fragment dwords (e0,e4) (e1,e5) (e2,e6) (e3,e7)
+__device__ __forceinline__ uint4 pack_kslots(const float (&e)[8]) {
+  return make_uint4(cvt2(e[0], e[4]), cvt2(e[1], e[5]), cvt2(e[2], e[6]), cvt2(e[3], e[7]));
 }
 
-// INT8: elements 0-3 in d0, 4-7 in d1 (little-endian bytes)
+// INT4 exact: bf16_rne(fp32(q) * s) (dq_int4x8; FAST needs dq_fast_ok(s))
+template <bool FAST>
+__device__ __forceinline__ uint4 b_int4_exact(uint32_t w, float s, const DqScale &d) {
+  float e[8];
+  if constexpr (FAST)
+    dq_int4x8(w, d, e);
+  else
+    dq_slow_int4x8(w, s, e);
+  return pack_kslots(e);
+}
+
 __device__ __forceinline__ uint4 b_int8_folded(uint32_t d0, uint32_t d1) {
   const uint32_t u = d0 ^ 0x80808080u, v = d1 ^ 0x80808080u;  // q + 128
   return make_uint4(cvt2(static_cast<float>(u & 0xFF), static_cast<float>(v & 0xFF)),
@@ -154,14 +144,29 @@ __device__ __forceinline__ uint4 b_int8_folded(uint32_t d0, uint32_t d1) {
                     cvt2(static_cast<float>(u >> 24), static_cast<float>(v >> 24)));
 }
 
-__device__ __forceinline__ uint4 b_int8_exact(uint32_t d0, uint32_t d1, float s, float c) {
-  const uint32_t u = d0 ^ 0x80808080u, v = d1 ^ 0x80808080u;
-  auto f = [&](uint32_t byte) { return fmaf(static_cast<float>(byte), s, c); };
-  return make_uint4(cvt2(f(u & 0xFF), f(v & 0xFF)), cvt2(f((u >> 8) & 0xFF), f((v >> 8) & 0xFF)),
-                    cvt2(f((u >> 16) & 0xFF), f((v >> 16) & 0xFF)), cvt2(f(u >> 24), f(v >> 24)));
+// INT8 exact: elements 0-3 in d0, 4-7 in d1
+template <bool FAST>
+__device__ __forceinline__ uint4 b_int8_exact(uint32_t d0, uint32_t d1, float s, const DqScale &d) {
+  float lo[4], hi[4];
+  if constexpr (FAST) {
+    dq_int8x4(d0, d, lo);
+    dq_int8x4(d1, d, hi);
+  } else {
+    dq_slow_int8x4(d0, s, lo);
+    dq_slow_int8x4(d1, s, hi);
+  }
+  return make_uint4(cvt2(lo[0], hi[0]), cvt2(lo[1], hi[1]), cvt2(lo[2], hi[2]), cvt2(lo[3], hi[3]));
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// raw buffer resource over [base, base + bytes) (gfx9 descriptor word 3);
+// loads at offsets >= bytes return zeros and touch no memory
+constexpr int kOutOfRange = 0x7FFFFFF0;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0,
+                                           static_cast<int>(bytes < kOutOfRange ? bytes : kOutOfRange), 0x00020000);
+}
 
 
 __device__ __forceinline__ float bf16_round(float v) {
@@ -187,8 +192,8 @@ struct WChunk<8> {
 template <int BITS, bool FOLDED, int NRT, bool FIRST>
 __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, int row0, int rows,
                                           unsigned char *lds) {
-  constexpr int kDepth = depth_for<NRT>();
-  static_assert(kDepth == 2 || kDepth == 4, "the K loop is unrolled for depth 2 or 4");
+  constexpr int kD = depth_for<BITS>();
+  static_assert(kD == 2 || kD == 4, "the K loop is unrolled for depth 2 or 4");
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
@@ -197,22 +202,26 @@ __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, in
   const int K = FIRST ? a.H : a.I;
   const int nk = (K + kKC - 1) / kKC;
 
-  // ---- staging (all four waves): a chunk is NRT*16 rows x 16 chunks of 16
-  // bytes; wave w, lane l owns pieces w*64 + l + 256q (q < NRT): row
-  // (w*64 + l + 256q) >> 4, 16-byte chunk c = l & 15, stored at LDS slot
+  // ---- token rows (all four waves stage them): a chunk is NRT*16 rows x 16
+  // pieces of 16 bytes; wave w, lane l owns pieces w*64 + l + 256q (q < NRT):
+  // row (w*64 + l + 256q) >> 4, piece c = l & 15, stored at LDS slot
   // c ^ (row & 15) of the row (XOR swizzle: conflict-free fragment reads).
-  // Rows arrive already K-slot permuted (xperm, act).  A chunk is loaded into
-  // registers two steps before it is consumed and written to LDS one step
-  // before, so these loads never stall the weight prefetch.
-  const uint16_t *abase = FIRST ? a.xperm : a.act;
-  int srcoff[NRT];  // element offset of each owned row (row 0 for padding rows)
+  // Rows arrive already K-slot permuted (xperm, act).
+  // Every load below is a raw buffer load: a chunk index past the end maps
+  // to an offset past the buffer's size, which the hardware answers with
+  // zeros without touching memory.  The K loop therefore issues the same
+  // loads in every step (straight-line code, so the compiler counts the loads
+  // in flight exactly) and no step ever reads outside its operands.
+  const __amdgpu_buffer_rsrc_t arsrc = make_rsrc(FIRST ? static_cast<const void *>(a.xperm) : a.act,
+                                                 FIRST ? a.T * a.H * 2 : a.T * a.k * a.I * 2);
+  int srcoff[NRT];  // byte offset of each owned row piece (row 0 for padding rows)
   int ldsoff[NRT];  // byte offset of each owned piece within a stage
 #pragma unroll
   for (int q = 0; q < NRT; ++q) {
     const int piece = wave * 64 + lane + 256 * q;
     const int r = piece >> 4;
     const int rr = r < rows ? r : 0;
-    srcoff[q] = (FIRST ? (a.sorted[row0 + rr] / a.k) * a.H : (row0 + rr) * a.I) + 8 * (lane & 15);
+    srcoff[q] = 2 * ((FIRST ? (a.sorted[row0 + rr] / a.k) * a.H : (row0 + rr) * a.I) + 8 * (lane & 15));
     ldsoff[q] = r * kRowBytes + 16 * ((lane & 15) ^ (r & 15));
   }
   auto load_a = [&](int i, u32x4(&v)[NRT]) __attribute__((always_inline)) {
@@ -221,7 +230,7 @@ __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, in
       int kk = i * kKC;
       // K tail: the chunk is past the row end; any finite in-row value (its B is zero)
       kk = kk + 8 * (lane & 15) < K ? kk : K - 8 - 8 * (lane & 15);
-      v[q] = *reinterpret_cast<const u32x4 *>(abase + srcoff[q] + kk);
+      v[q] = __builtin_amdgcn_raw_buffer_load_b128(arsrc, i < nk ? srcoff[q] + 2 * kk : kOutOfRange, 0, 0);
     }
   };
   auto store_a = [&](int i, const u32x4(&v)[NRT]) __attribute__((always_inline)) {
@@ -231,12 +240,15 @@ __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, in
   };
 
   // ---- weights: wave w owns two 16-row tiles
-  const int64_t rowbytes = BITS == 4 ? (K >> 1) : K;
+  const int rowbytes = BITS == 4 ? (K >> 1) : K;
   const int G = FIRST ? a.g1 : a.g2;
   const int ng = FIRST ? a.ng1 : a.ng2;
   const int nrows_w = FIRST ? 2 * a.I : a.H;
-  const int8_t *W = (FIRST ? a.q1 : a.q2) + static_cast<int64_t>(e) * nrows_w * rowbytes;
-  const float *S = (FIRST ? a.s1 : a.s2) + static_cast<int64_t>(e) * nrows_w * ng;
+  const __amdgpu_buffer_rsrc_t wrsrc =
+      make_rsrc((FIRST ? a.q1 : a.q2) + static_cast<int64_t>(e) * nrows_w * rowbytes,
+                static_cast<int64_t>(nrows_w) * rowbytes);
+  const __amdgpu_buffer_rsrc_t srsrc = make_rsrc((FIRST ? a.s1 : a.s2) + static_cast<int64_t>(e) * nrows_w * ng,
+                                                 static_cast<int64_t>(nrows_w) * ng * 4);
   int wr[2];
   if (FIRST) {
     wr[0] = slice * kF1 + 16 * wave + lc;        // gate row
@@ -245,24 +257,25 @@ __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, in
     wr[0] = slice * kR2 + 32 * wave + lc;
     wr[1] = wr[0] + 16;
   }
-  const int8_t *wp[2] = {W + wr[0] * rowbytes, W + wr[1] * rowbytes};
-  const float *sp[2] = {S + static_cast<int64_t>(wr[0]) * ng, S + static_cast<int64_t>(wr[1]) * ng};
+  const int woff[2] = {wr[0] * rowbytes, wr[1] * rowbytes};
+  const int soff[2] = {wr[0] * ng * 4, wr[1] * ng * 4};
 
   auto load_w = [&](int i, WChunk<BITS>(&w)[2], float(&sc)[2]) __attribute__((always_inline)) {
     const int kelem = i * kKC + 32 * lg;
-    const bool ok = kelem < K;
-    const int ke = ok ? kelem : 0;  // K tail: a valid address, the value is discarded
-    const int sidx = (FOLDED ? i * kKC : ke) / G;
+    const bool ok = i < nk && kelem < K;  // K tail lanes and chunks past the end read zeros
+    const int sidx = (FOLDED ? i * kKC : kelem) / G;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       if constexpr (BITS == 4) {
-        w[c].v = *reinterpret_cast<const uint4 *>(wp[c] + (ke >> 1));
+        w[c].v = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, ok ? woff[c] + (kelem >> 1) : kOutOfRange, 0, 0));
       } else {
-        const uint4 *p = reinterpret_cast<const uint4 *>(wp[c] + ke);
-        w[c].v0 = p[0];
-        w[c].v1 = p[1];
+        const int o = ok ? woff[c] + kelem : kOutOfRange;
+        w[c].v0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, o, 0, 0));
+        w[c].v1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, o + (ok ? 16 : 0), 0, 0));
       }
-      sc[c] = sp[c][sidx];
+      sc[c] = __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(srsrc, ok ? soff[c] + 4 * sidx : kOutOfRange, 0, 0));
     }
   };
 
@@ -273,23 +286,21 @@ __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, in
     for (int c = 0; c < 2; ++c) tot[rt][c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
   // one 128-wide K chunk of this wave's two tiles against the staged rows;
-  // TAIL: the chunk may run past K (K % 128 != 0), lanes past it feed zeros
-  auto compute = [&](int i, const WChunk<BITS>(&w)[2], const float(&sc)[2], auto tail_tag)
+  // TAIL: the chunk may run past K (K % 128 != 0), lanes past it feed zeros;
+  // FAST: every lane's scales pass dq_fast_ok (wave-uniform choice)
+  auto compute_body = [&](int i, const WChunk<BITS>(&w)[2], const float(&sc)[2], auto tail_tag, auto fast_tag)
       __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail_tag)::value;
+    constexpr bool FAST = decltype(fast_tag)::value;
     const unsigned char *buf = lds + (i % kStages) * kStageBytes;
     const bool kvalid = !TAIL || i * kKC + 32 * lg < K;
-    constexpr float kOff = BITS == 4 ? 8.0f : 128.0f;
     const uint32_t one2 = kvalid ? 0x3F803F80u : 0u;  // bf16 1.0 pairs; zero past the K tail
     const uint4 ones4 = make_uint4(one2, one2, one2, one2);
     floatx4 acc[NRT][2];
     floatx4 xs[NRT];
-    float cexact[2], s16[2];
+    DqScale dqs[2];
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      cexact[c] = -kOff * sc[c];
-      s16[c] = sc[c] * 0.0625f;
-    }
+    for (int c = 0; c < 2; ++c) dqs[c] = dq_scale<BITS>(sc[c]);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       uint4 b[2];
@@ -297,12 +308,18 @@ __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, in
       for (int c = 0; c < 2; ++c) {
         if constexpr (BITS == 4) {
           const uint32_t q = s == 0 ? w[c].v.x : s == 1 ? w[c].v.y : s == 2 ? w[c].v.z : w[c].v.w;
-          b[c] = FOLDED ? b_int4_folded(q) : b_int4_exact(q, sc[c], s16[c], cexact[c]);
+          if constexpr (FOLDED)
+            b[c] = b_int4_folded(q);
+          else
+            b[c] = b_int4_exact<FAST>(q, sc[c], dqs[c]);
         } else {
           const uint4 &v = s < 2 ? w[c].v0 : w[c].v1;
           const uint32_t d0 = (s & 1) ? v.z : v.x;
           const uint32_t d1 = (s & 1) ? v.w : v.y;
-          b[c] = FOLDED ? b_int8_folded(d0, d1) : b_int8_exact(d0, d1, sc[c], cexact[c]);
+          if constexpr (FOLDED)
+            b[c] = b_int8_folded(d0, d1);
+          else
+            b[c] = b_int8_exact<FAST>(d0, d1, sc[c], dqs[c]);
         }
         if constexpr (TAIL) {
           if (!kvalid) b[c] = make_uint4(0, 0, 0, 0);
@@ -310,7 +327,7 @@ __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, in
       }
 #pragma unroll
       for (int rt = 0; rt < NRT; ++rt) {
-        // row rt*16 + lc (its low 4 bits are lc), K chunk 4*lg + s of this 128-wide chunk
+        // row rt*16 + lc (its low 4 bits are lc), K piece 4*lg + s of this 128-wide chunk
         const uint4 af = *reinterpret_cast<const uint4 *>(buf + (rt * 16 + lc) * kRowBytes +
                                                           16 * ((4 * lg + s) ^ lc));
         if constexpr (!FOLDED) {
@@ -341,54 +358,60 @@ __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, in
             tot[rt][c][j] = fmaf(sc[c], fmaf(-kBias, xs[rt][j], acc[rt][c][j]), tot[rt][c][j]);
     }
   };
+  auto compute = [&](int i, const WChunk<BITS>(&w)[2], const float(&sc)[2], auto tail_tag)
+      __attribute__((always_inline)) {
+    if constexpr (FOLDED) {
+      compute_body(i, w, sc, tail_tag, std::true_type{});
+    } else {
+      if (__all(dq_fast_ok(sc[0]) && dq_fast_ok(sc[1])))
+        compute_body(i, w, sc, tail_tag, std::true_type{});
+      else
+        compute_body(i, w, sc, tail_tag, std::false_type{});
+    }
+  };
 
-  // Issue order per step i: A(i+2) into registers, compute chunk i, weights
-  // of chunk i+D, A(i+1) registers -> LDS, barrier.
-  WChunk<BITS> wb[kDepth][2];
-  float sb[kDepth][2];
+  // Prefetch schedule.  Every vector load of a wave completes in issue order
+  // (one vmcnt counter), so waiting for a token chunk also waits for every
+  // weight load issued before it.  Token chunk i+1 (stored to LDS in step i)
+  // is therefore issued together with, and just before, weight chunk i
+  // (consumed in step i): kD steps ahead, in the register slot that step i
+  // frees.  Waiting for either never drains the kD - 1 younger weight chunks.
+  //   step i: compute chunk i (weights slot i % kD, tokens LDS stage i % 2);
+  //           tokens i+1: slot -> LDS stage (i+1) % 2; issue tokens i+1+kD
+  //           into that slot; issue weights i+kD into slot i % kD; barrier.
+  WChunk<BITS> wb[kD][2];
+  float sb[kD][2];
+  u32x4 av[kD][NRT];
 #pragma unroll
-  for (int d = 0; d < kDepth; ++d)
-    if (d < nk) load_w(d, wb[d], sb[d]);
-  u32x4 av[2][NRT];
-  load_a(0, av[0]);
-  if (nk > 1) load_a(1, av[1]);
+  for (int d = 0; d < kD; ++d) {
+    load_a(d, av[d]);
+    load_w(d, wb[d], sb[d]);
+  }
   store_a(0, av[0]);
+  load_a(kD, av[0]);
   __syncthreads();  // chunk 0 staged
 
-  // One K step: stage A(i+2), compute chunk i, prefetch weights of chunk
-  // i+D, write A(i+1) to LDS.  In the steady state every load is issued
-  // unconditionally (straight-line code lets the compiler count the memory
-  // operations still in flight exactly instead of draining them); the last
-  // steps run the guarded form.  (kDepth is even, so step parity = d parity
-  // and the register buffers are static.)
-  auto step = [&](int i, auto d_tag, auto steady_tag) __attribute__((always_inline)) {
+  // One step per chunk, kD steps per loop iteration (static register slots).
+  // Steps past the last chunk (nk % kD != 0) compute nothing; their loads
+  // are out of range.  The branches below contain no loads.
+  auto step = [&](int i, auto d_tag) __attribute__((always_inline)) {
     constexpr int d = decltype(d_tag)::value;
-    constexpr bool steady = decltype(steady_tag)::value;
-    if (steady || i + 2 < nk) load_a(i + 2, av[d & 1]);
-    if (steady || (K % kKC) == 0 || i + 1 < nk)
+    constexpr int dn = (d + 1) % kD;
+    if (i + 1 < nk || (i + 1 == nk && (K % kKC) == 0))
       compute(i, wb[d], sb[d], std::false_type{});
-    else
+    else if (i + 1 == nk)
       compute(i, wb[d], sb[d], std::true_type{});  // the partial last chunk
-    if (steady || i + kDepth < nk) load_w(i + kDepth, wb[d], sb[d]);
-    if (steady || i + 1 < nk) store_a(i + 1, av[(d + 1) & 1]);
+    store_a(i + 1, av[dn]);
+    load_a(i + 1 + kD, av[dn]);
+    load_w(i + kD, wb[d], sb[d]);
     __syncthreads();  // chunk i consumed by every wave, chunk i + 1 staged
   };
-  int i0 = 0;
-  // steady blocks: every step of the block has i + kDepth < nk (and so i + 2 < nk)
-  for (; i0 + 2 * kDepth - 1 < nk; i0 += kDepth) {
-    step(i0 + 0, std::integral_constant<int, 0>{}, std::true_type{});
-    step(i0 + 1, std::integral_constant<int, 1>{}, std::true_type{});
-    if constexpr (kDepth > 2) {
-      step(i0 + 2, std::integral_constant<int, 2>{}, std::true_type{});
-      step(i0 + 3, std::integral_constant<int, 3>{}, std::true_type{});
-    }
-  }
-  for (; i0 < nk; i0 += kDepth) {
-    step(i0 + 0, std::integral_constant<int, 0>{}, std::false_type{});
-    if (i0 + 1 < nk) step(i0 + 1, std::integral_constant<int, 1>{}, std::false_type{});
-    if constexpr (kDepth > 2) {
-      if (i0 + 2 < nk) step(i0 + 2, std::integral_constant<int, 2>{}, std::false_type{});
-      if (i0 + 3 < nk) step(i0 + 3, std::integral_constant<int, 3>{}, std::false_type{});
+  for (int i0 = 0; i0 < nk; i0 += kD) {
+    step(i0 + 0, std::integral_constant<int, 0>{});
+    step(i0 + 1, std::integral_constant<int, 1>{});
+    if constexpr (kD > 2) {
+      step(i0 + 2, std::integral_constant<int, 2>{});
+      step(i0 + 3, std::integral_constant<int, 3>{});
     }
   }
 
@@ -466,39 +489,31 @@ __global__ __launch_bounds__(kCombineBlock) void combine_kernel(const float *__r
   *reinterpret_cast<uint4 *>(out + base) = make_uint4(p[0], p[1], p[2], p[3]);
 }
 
-// Persistent G1 (FIRST) or G2 kernel: each workgroup takes items of its phase
-// in ticket order until the phase's list is exhausted.
+// Persistent G1 (FIRST) or G2 kernel.  Items are (row block, slice) pairs,
+// block-major: item t is slice t % per of block t / per.  The list is cut
+// into 8 contiguous ranges, one per XCD (workgroup g runs on XCD g % 8), so
+// the slices of one row block -- which stage the same token rows -- and the
+// row blocks of one expert -- which read the same weights at about the same
+// time -- meet in one L2.  Workgroups of an XCD take its items round-robin;
+// the grid is a multiple of 8.
 template <int BITS, bool FOLDED, bool FIRST>
 __global__ __launch_bounds__(kThreads, 2) void moe_gemm_kernel(MoeArgs a) {
   __shared__ __align__(16) unsigned char lds[kStages * kStageBytes];
-  __shared__ int s_item;
-  const int tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lane = tid & 63;
-  const int n_items = __builtin_amdgcn_readfirstlane(FIRST ? a.hdr->n_g1 : a.hdr->n_g2);
-  const uint2 *items = a.items + (FIRST ? 0 : __builtin_amdgcn_readfirstlane(a.hdr->n_g1));
-  int32_t *ticket = &a.hdr->ticket[FIRST ? 0 : 1];
-  // Every branch of this loop is wave-uniform.  (A lane-divergent
-  // `if (tid == 0)` here lets the compiler split the loop so that lanes
-  // other than 0 re-enter the item body without a new ticket.)
-  for (;;) {
-    if (wave == 0) {
-      // lane 0 takes the ticket; the other lanes add 0 and read the same word
-      const int mine = __hip_atomic_fetch_add(ticket, lane == 0 ? 1 : 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s_item = __builtin_amdgcn_readfirstlane(mine);
-    }
-    __syncthreads();
-    // every value below is wave-uniform (scalar): the branches it feeds contain barriers
-    const int t = __builtin_amdgcn_readfirstlane(s_item);
-    __syncthreads();
-    if (t >= n_items) break;
-    const uint2 it = items[t];
-    const uint32_t ix = __builtin_amdgcn_readfirstlane(it.x);
-    const int e = static_cast<int>(ix & 0xFFu);
-    const int slice = static_cast<int>(ix >> 8);
-    const int blk = static_cast<int>(__builtin_amdgcn_readfirstlane(it.y));
-    const int row0 = __builtin_amdgcn_readfirstlane(a.offsets[e] + blk * kRowsMax);
-    const int rows = __builtin_amdgcn_readfirstlane(min(kRowsMax, a.offsets[e + 1] - row0));
+  const int nb = __builtin_amdgcn_readfirstlane(a.hdr->n_blk);
+  const int per = FIRST ? a.I / kF1 : a.H / kR2;
+  const int n = nb * per;
+  const int xcd = blockIdx.x & 7;
+  const int gx = gridDim.x >> 3;
+  const int n8 = (n + 7) >> 3;
+  const int end = min(n, (xcd + 1) * n8);
+  // every value below is wave-uniform (scalar): the item body contains barriers
+  for (int t = xcd * n8 + static_cast<int>(blockIdx.x >> 3); t < end; t += gx) {
+    const int blk = t / per;
+    const int slice = t - blk * per;
+    const int4 bi = a.blocks[blk];
+    const int e = __builtin_amdgcn_readfirstlane(bi.x);
+    const int row0 = __builtin_amdgcn_readfirstlane(bi.y);
+    const int rows = __builtin_amdgcn_readfirstlane(bi.z);
     gemm_dispatch<BITS, FOLDED, FIRST>(a, e, slice, row0, rows, lds);
   }
 }
@@ -517,11 +532,9 @@ struct PlanArgs {
   int32_t *counts;
   int32_t *offsets;
   int32_t *sorted;
-  // work list (items == nullptr: permutation only)
-  uint2 *items;
+  // block table (blocks == nullptr: permutation only)
+  int4 *blocks;
   PlanHeader *hdr;
-  int nf;  // G1 slices per expert (I / kF1)
-  int nr;  // G2 slices per expert (H / kR2)
 };
 
 // exclusive scan of in[0..E) by wave 0 (lane l owns entries 4l..4l+3)
@@ -578,38 +591,27 @@ __global__ __launch_bounds__(kPlanBlock) void plan_kernel(PlanArgs p) {
   }
   if (tid == 0) p.offsets[E] = total;
 
-  if (p.items != nullptr) {
+  if (p.blocks != nullptr) {
     // row blocks per expert and their scan
     for (int e = tid; e < E; e += kPlanBlock) wcnt[0][e] = (hist[e] + kRowsMax - 1) / kRowsMax;
     __syncthreads();
     if (wave == 0) wave0_exclusive_scan(wcnt[0], nbs, E, &nbs[E]);
     __syncthreads();
+    // block table, expert-major: block b of expert e covers sorted rows
+    // [offsets[e] + 32 j, +32) with j = b - nbs[e]
     const int nb_total = nbs[E];
-    const int n_g1 = nb_total * p.nf;
-    const int n_g2 = nb_total * p.nr;
-    const int n_items = n_g1 + n_g2;
-    for (int t = tid; t < n_items; t += kPlanBlock) {
-      const bool g1 = t < n_g1;
-      const int per = g1 ? p.nf : p.nr;
-      const int local = g1 ? t : t - n_g1;
-      const int bidx = local / per;  // global row-block index (expert-major)
-      int lo = 0, hi = E;            // largest e with nbs[e] <= bidx
+    for (int b = tid; b < nb_total; b += kPlanBlock) {
+      int lo = 0, hi = E;  // largest e with nbs[e] <= b
       while (hi - lo > 1) {
         const int mid = (lo + hi) >> 1;
-        if (nbs[mid] <= bidx) lo = mid;
+        if (nbs[mid] <= b) lo = mid;
         else hi = mid;
       }
       const int e = lo;
-      const int nb = nbs[e + 1] - nbs[e];
-      const int within = local - nbs[e] * per;  // slice-major, block-minor
-      p.items[t] = item_code(e, within / nb, within % nb);
+      const int r0 = base[e] + (b - nbs[e]) * kRowsMax;
+      p.blocks[b] = make_int4(e, r0, min(kRowsMax, base[e] + hist[e] - r0), 0);
     }
-    if (tid == 0) {
-      p.hdr->ticket[0] = 0;
-      p.hdr->ticket[1] = 0;
-      p.hdr->n_g1 = n_g1;
-      p.hdr->n_g2 = n_g2;
-    }
+    if (tid == 0) p.hdr->n_blk = nb_total;
     __syncthreads();
     for (int e = tid; e < E; e += kPlanBlock) wcnt[0][e] = 0;
   }
@@ -666,15 +668,15 @@ __global__ __launch_bounds__(256) void permute_rows_kernel(const uint16_t *__res
 // ---------------------------------------------------------------------------
 
 struct WsLayout {
-  size_t counts, offsets, sorted, hdr, items, ids, weights, xperm, act, ybuf, total;
+  size_t counts, offsets, sorted, hdr, blocks, ids, weights, xperm, act, ybuf, total;
 };
 
 inline size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
-int64_t max_items_for(int64_t T, int H, int I, int E, int k) {
+// row blocks of at most kRowsMax sorted rows: one partial block per expert at most
+int64_t max_blocks_for(int64_t T, int E, int k) {
   const int64_t N = T * k;
-  const int64_t blocks = std::min<int64_t>(E, N) + N / kRowsMax;
-  return blocks * (I / kF1 + H / kR2);
+  return std::min<int64_t>(E, N) + N / kRowsMax;
 }
 
 WsLayout ws_layout(int64_t T, int H, int I, int E, int k) {
@@ -689,7 +691,7 @@ WsLayout ws_layout(int64_t T, int H, int I, int E, int k) {
   take(w.offsets, sizeof(int32_t) * (E + 1));
   take(w.sorted, sizeof(int32_t) * N);
   take(w.hdr, sizeof(PlanHeader));
-  take(w.items, sizeof(uint2) * max_items_for(T, H, I, E, k));
+  take(w.blocks, sizeof(int4) * max_blocks_for(T, E, k));
   take(w.ids, sizeof(int32_t) * N);
   take(w.weights, sizeof(float) * N);
   take(w.xperm, sizeof(uint16_t) * T * H);
@@ -701,7 +703,8 @@ WsLayout ws_layout(int64_t T, int H, int I, int E, int k) {
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-// persistent grid: resident workgroups of one GEMM kernel on this device
+// persistent grid: resident workgroups of one GEMM kernel on this device,
+// a multiple of 8 (one share per XCD), no more than the items can use
 template <int BITS, bool FOLDED, bool FIRST>
 int gemm_grid(int64_t max_items) {
   static int cached[64] = {0};
@@ -718,7 +721,8 @@ int gemm_grid(int64_t max_items) {
     g = cus * per_cu;
     cached[dev] = g;
   }
-  return static_cast<int>(std::min<int64_t>(g, std::max<int64_t>(max_items, 1)));
+  const int64_t want = (std::max<int64_t>(max_items, 1) + 7) / 8 * 8;
+  return static_cast<int>(std::max<int64_t>(8, std::min<int64_t>(g / 8 * 8, want)));
 }
 
 // Measurement hook (lq_moe_profile_events): caller-owned hipEvent_t handles
@@ -758,10 +762,15 @@ int validate_layer(const void *x, int64_t T, int H, int I, int E, int k, const i
                 "moe_forward: the group length along K must be a multiple of 32 (got " + std::to_string(g1) +
                     " for w1, " + std::to_string(g2) + " for w2)");
   const int64_t N = T * k;
-  if (T > (int64_t{1} << 18) || N * static_cast<int64_t>(H > I ? H : I) > 0x7FFFFFFFll ||
-      T * static_cast<int64_t>(H) > 0x7FFFFFFFll)
+  // the GEMMs address x, act, one expert's codes and one expert's scales
+  // through 32-bit buffer offsets below kOutOfRange
+  if (T > (int64_t{1} << 18) || N * static_cast<int64_t>(H > I ? H : I) * 4 > 0x7FFFFFFFll ||
+      T * static_cast<int64_t>(H) * 2 >= kOutOfRange)
     return fail(LQ_ERR_UNSUPPORTED, "moe_forward: too many tokens for one call");
-  if (max_items_for(T, H, I, E, k) > 0x3FFFFFFF) return fail(LQ_ERR_UNSUPPORTED, "moe_forward: work list too long");
+  if (int64_t{2} * I * H >= kOutOfRange)
+    return fail(LQ_ERR_UNSUPPORTED, "moe_forward: one expert's weights exceed 2 GiB");
+  if (max_blocks_for(T, E, k) * (I / kF1 + H / kR2) > 0x3FFFFFFF)
+    return fail(LQ_ERR_UNSUPPORTED, "moe_forward: work list too long");
   if (T == 0) return LQ_OK;
   if (!x || !q1 || !s1 || !q2 || !s2 || !workspace || !out) return fail(LQ_ERR_VALUE, "moe_forward: null pointer");
   if (!aligned16(x) || !aligned16(q1) || !aligned16(q2) || !aligned16(workspace) || !aligned16(out))
@@ -813,10 +822,8 @@ int moe_forward_impl(const void *x, bool x_permuted, int64_t T, int H, int I, in
   p.counts = reinterpret_cast<int32_t *>(ws + w.counts);
   p.offsets = reinterpret_cast<int32_t *>(ws + w.offsets);
   p.sorted = reinterpret_cast<int32_t *>(ws + w.sorted);
-  p.items = reinterpret_cast<uint2 *>(ws + w.items);
+  p.blocks = reinterpret_cast<int4 *>(ws + w.blocks);
   p.hdr = reinterpret_cast<PlanHeader *>(ws + w.hdr);
-  p.nf = I / kF1;
-  p.nr = H / kR2;
   uint16_t *xperm = reinterpret_cast<uint16_t *>(ws + w.xperm);
   if (!x_permuted) {
     const int64_t n8 = T * H / 8;
@@ -838,7 +845,7 @@ int moe_forward_impl(const void *x, bool x_permuted, int64_t T, int H, int I, in
   a.topk_w = topk_weights;
   a.offsets = p.offsets;
   a.sorted = p.sorted;
-  a.items = p.items;
+  a.blocks = p.blocks;
   a.hdr = p.hdr;
   a.act = reinterpret_cast<uint16_t *>(ws + w.act);
   a.ybuf = reinterpret_cast<float *>(ws + w.ybuf);
@@ -852,7 +859,7 @@ int moe_forward_impl(const void *x, bool x_permuted, int64_t T, int H, int I, in
   a.ng1 = static_cast<int>(H / g1);
   a.g2 = static_cast<int>(g2);
   a.ng2 = static_cast<int>(I / g2);
-  const int64_t blocks = std::min<int64_t>(E, N) + N / kRowsMax;
+  const int64_t blocks = max_blocks_for(T, E, k);
   const int64_t max_g1 = blocks * (I / kF1), max_g2 = blocks * (H / kR2);
   if (bits == 4)
     rc = folded ? launch_phases<4, true>(a, max_g1, max_g2, st, pm, first_mark)
@@ -882,7 +889,7 @@ int launch_permute(const int32_t *ids, int64_t N, int E, int32_t *counts, int32_
   p.counts = counts;
   p.offsets = offsets;
   p.sorted = sorted;
-  p.items = nullptr;
+  p.blocks = nullptr;
   plan_kernel<<<1, kPlanBlock, 0, st>>>(p);
   return check_launch("moe_permute");
 }

@@ -90,21 +90,30 @@ __global__ __launch_bounds__(kBlock) void dequant8_kernel(
     const int64_t row = c / cpr;
     const int64_t col = (c - row * cpr) << 3;
     const float sc = load_f32<SDT>(s, row * ng + col / g);
+    // the products come from the same routine the MoE GEMMs feed their
+    // matrix cores with (dq_int4x8 / dq_int8x4)
     float v[8];
     if constexpr (BITS == 4) {
       const uint32_t w = *reinterpret_cast<const uint32_t *>(q + row * (k >> 1) + (col >> 1));
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int32_t n = static_cast<int32_t>(w << (28 - 4 * i)) >> 28;
-        v[i] = static_cast<float>(n) * sc;
-      }
+      if (dq_fast_ok(sc))
+        dq_int4x8(w, dq_scale<4>(sc), v);
+      else
+        dq_slow_int4x8(w, sc, v);
     } else {
       const uint2 w = *reinterpret_cast<const uint2 *>(q + row * k + col);
+      float lo[4], hi[4];
+      if (dq_fast_ok(sc)) {
+        const DqScale d = dq_scale<8>(sc);
+        dq_int8x4(w.x, d, lo);
+        dq_int8x4(w.y, d, hi);
+      } else {
+        dq_slow_int8x4(w.x, sc, lo);
+        dq_slow_int8x4(w.y, sc, hi);
+      }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t word = i < 4 ? w.x : w.y;
-        const int32_t n = static_cast<int32_t>(word << (24 - 8 * (i & 3))) >> 24;
-        v[i] = static_cast<float>(n) * sc;
+      for (int i = 0; i < 4; ++i) {
+        v[i] = lo[i];
+        v[4 + i] = hi[i];
       }
     }
     store8<SDT, ODT>(out, row * k + col, v);
