@@ -91,6 +91,7 @@ struct MoeArgs {
   const float *topk_w;     // [T*k]
   const int32_t *offsets;  // [E+1]
   const int32_t *sorted;   // [T*k] assignment ids by expert
+  const int32_t *srow;     // [T*k] token of each sorted row (sorted / k)
   const int4 *blocks;      // row blocks {expert, first sorted row, rows, 0}
   const PlanHeader *hdr;
   uint16_t *act;           // [T*k, I] bf16, by sorted row
@@ -189,7 +190,7 @@ struct WChunk<8> {
 // one G1 / G2 item
 // ---------------------------------------------------------------------------
 
-template <int BITS, bool FOLDED, int NRT, bool FIRST>
+template <int BITS, bool FOLDED, int NRT, bool FIRST, bool G128>
 __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, int row0, int rows,
                                           unsigned char *lds) {
   constexpr int kD = depth_for<BITS>();
@@ -207,31 +208,38 @@ __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, in
   // row (w*64 + l + 256q) >> 4, piece c = l & 15, stored at LDS slot
   // c ^ (row & 15) of the row (XOR swizzle: conflict-free fragment reads).
   // Rows arrive already K-slot permuted (xperm, act).
-  // Every load below is a raw buffer load: a chunk index past the end maps
-  // to an offset past the buffer's size, which the hardware answers with
-  // zeros without touching memory.  The K loop therefore issues the same
-  // loads in every step (straight-line code, so the compiler counts the loads
-  // in flight exactly) and no step ever reads outside its operands.
+  // Every load below is a raw buffer load.  The per-lane byte offset is
+  // fixed for the item; the chunk's offset rides in the wave-uniform soffset.
+  // Steps past the last chunk load through an empty descriptor (size 0),
+  // which the hardware answers with zeros without touching memory, so the K
+  // loop issues the same loads in every step (straight-line code: the
+  // compiler counts the loads in flight exactly) and never reads outside its
+  // operands.  Only the partial last chunk of a K that is not a multiple of
+  // 128 takes per-lane offsets (ktail).
+  const bool ktail = (K % kKC) != 0;
   const __amdgpu_buffer_rsrc_t arsrc = make_rsrc(FIRST ? static_cast<const void *>(a.xperm) : a.act,
                                                  FIRST ? a.T * a.H * 2 : a.T * a.k * a.I * 2);
-  int srcoff[NRT];  // byte offset of each owned row piece (row 0 for padding rows)
-  int ldsoff[NRT];  // byte offset of each owned piece within a stage
+  int avoff[NRT];    // byte offset of each owned row piece in chunk 0 (row 0 for padding rows)
+  int avoff_t[NRT];  // the same for the partial last chunk, clamped into the row
+  int ldsoff[NRT];   // byte offset of each owned piece within a stage
 #pragma unroll
   for (int q = 0; q < NRT; ++q) {
     const int piece = wave * 64 + lane + 256 * q;
     const int r = piece >> 4;
     const int rr = r < rows ? r : 0;
-    srcoff[q] = 2 * ((FIRST ? (a.sorted[row0 + rr] / a.k) * a.H : (row0 + rr) * a.I) + 8 * (lane & 15));
+    const int rowelem = FIRST ? a.srow[row0 + rr] * a.H : (row0 + rr) * a.I;
+    avoff[q] = 2 * (rowelem + 8 * (lane & 15));
+    // lanes past the row end read its last 8 values (finite; their B is zero)
+    avoff_t[q] = 2 * (rowelem + min(8 * (lane & 15), K - 8 - (nk - 1) * kKC));
     ldsoff[q] = r * kRowBytes + 16 * ((lane & 15) ^ (r & 15));
   }
+  const __amdgpu_buffer_rsrc_t empty = make_rsrc(a.out, 0);
   auto load_a = [&](int i, u32x4(&v)[NRT]) __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t r = i < nk ? arsrc : empty;
+    const bool tail = ktail && i == nk - 1;
 #pragma unroll
-    for (int q = 0; q < NRT; ++q) {
-      int kk = i * kKC;
-      // K tail: the chunk is past the row end; any finite in-row value (its B is zero)
-      kk = kk + 8 * (lane & 15) < K ? kk : K - 8 - 8 * (lane & 15);
-      v[q] = __builtin_amdgcn_raw_buffer_load_b128(arsrc, i < nk ? srcoff[q] + 2 * kk : kOutOfRange, 0, 0);
-    }
+    for (int q = 0; q < NRT; ++q)
+      v[q] = __builtin_amdgcn_raw_buffer_load_b128(r, tail ? avoff_t[q] : avoff[q], i * kKC * 2, 0);
   };
   auto store_a = [&](int i, const u32x4(&v)[NRT]) __attribute__((always_inline)) {
     unsigned char *buf = lds + (i % kStages) * kStageBytes;
@@ -257,25 +265,38 @@ __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, in
     wr[0] = slice * kR2 + 32 * wave + lc;
     wr[1] = wr[0] + 16;
   }
-  const int woff[2] = {wr[0] * rowbytes, wr[1] * rowbytes};
-  const int soff[2] = {wr[0] * ng * 4, wr[1] * ng * 4};
+  constexpr int kLaneBytes = BITS == 4 ? 16 : 32;  // one lane's 32 codes of a chunk
+  constexpr int kChunkBytes = BITS == 4 ? 64 : 128;
+  // lanes whose 32 K values of the partial last chunk lie past K read zeros
+  const bool lane_in_tail = (nk - 1) * kKC + 32 * lg < K;
+  int wvoff[2], wvoff_t[2], svoff[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    wvoff[c] = wr[c] * rowbytes + kLaneBytes * lg;
+    wvoff_t[c] = lane_in_tail ? wvoff[c] : kOutOfRange;
+    svoff[c] = wr[c] * ng * 4;
+  }
 
   auto load_w = [&](int i, WChunk<BITS>(&w)[2], float(&sc)[2]) __attribute__((always_inline)) {
-    const int kelem = i * kKC + 32 * lg;
-    const bool ok = i < nk && kelem < K;  // K tail lanes and chunks past the end read zeros
-    const int sidx = (FOLDED ? i * kKC : kelem) / G;
+    const __amdgpu_buffer_rsrc_t rw = i < nk ? wrsrc : empty;
+    const __amdgpu_buffer_rsrc_t rs = i < nk ? srsrc : empty;
+    const bool tail = ktail && i == nk - 1;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
+      const int vo = tail ? wvoff_t[c] : wvoff[c];
       if constexpr (BITS == 4) {
-        w[c].v = __builtin_bit_cast(
-            uint4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, ok ? woff[c] + (kelem >> 1) : kOutOfRange, 0, 0));
+        w[c].v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vo, i * kChunkBytes, 0));
       } else {
-        const int o = ok ? woff[c] + kelem : kOutOfRange;
-        w[c].v0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, o, 0, 0));
-        w[c].v1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, o + (ok ? 16 : 0), 0, 0));
+        w[c].v0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vo, i * kChunkBytes, 0));
+        w[c].v1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vo + 16, i * kChunkBytes, 0));
       }
-      sc[c] = __builtin_bit_cast(
-          float, __builtin_amdgcn_raw_buffer_load_b32(srsrc, ok ? soff[c] + 4 * sidx : kOutOfRange, 0, 0));
+      if constexpr (G128) {
+        sc[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, svoff[c], i * 4, 0));
+      } else {
+        // group of this lane's K values (FOLDED: of the chunk, G % 128 == 0)
+        const int sidx = (FOLDED ? i * kKC : min(i * kKC + 32 * lg, K - 1)) / G;
+        sc[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, svoff[c] + 4 * sidx, 0, 0));
+      }
     }
   };
 
@@ -285,17 +306,17 @@ __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, in
 #pragma unroll
     for (int c = 0; c < 2; ++c) tot[rt][c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // one 128-wide K chunk of this wave's two tiles against the staged rows;
-  // TAIL: the chunk may run past K (K % 128 != 0), lanes past it feed zeros;
-  // FAST: every lane's scales pass dq_fast_ok (wave-uniform choice)
-  auto compute_body = [&](int i, const WChunk<BITS>(&w)[2], const float(&sc)[2], auto tail_tag, auto fast_tag)
+  // one 128-wide K chunk of this wave's two tiles against the staged rows.
+  // FAST: every lane's scales pass dq_fast_ok (wave-uniform choice).  In
+  // the partial last chunk of a K that is not a multiple of 128, lanes past
+  // K loaded zero codes (out of range), which dequantize to +0 and meet
+  // finite token values; the folded form never sees such a chunk (it needs
+  // group lengths that are multiples of 128, hence K % 128 == 0).
+  auto compute_body = [&](int i, const WChunk<BITS>(&w)[2], const float(&sc)[2], auto fast_tag)
       __attribute__((always_inline)) {
-    constexpr bool TAIL = decltype(tail_tag)::value;
     constexpr bool FAST = decltype(fast_tag)::value;
     const unsigned char *buf = lds + (i % kStages) * kStageBytes;
-    const bool kvalid = !TAIL || i * kKC + 32 * lg < K;
-    const uint32_t one2 = kvalid ? 0x3F803F80u : 0u;  // bf16 1.0 pairs; zero past the K tail
-    const uint4 ones4 = make_uint4(one2, one2, one2, one2);
+    const uint4 ones4 = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);  // bf16 1.0
     floatx4 acc[NRT][2];
     floatx4 xs[NRT];
     DqScale dqs[2];
@@ -320,9 +341,6 @@ __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, in
             b[c] = b_int8_folded(d0, d1);
           else
             b[c] = b_int8_exact<FAST>(d0, d1, sc[c], dqs[c]);
-        }
-        if constexpr (TAIL) {
-          if (!kvalid) b[c] = make_uint4(0, 0, 0, 0);
         }
       }
 #pragma unroll
@@ -358,15 +376,14 @@ __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, in
             tot[rt][c][j] = fmaf(sc[c], fmaf(-kBias, xs[rt][j], acc[rt][c][j]), tot[rt][c][j]);
     }
   };
-  auto compute = [&](int i, const WChunk<BITS>(&w)[2], const float(&sc)[2], auto tail_tag)
-      __attribute__((always_inline)) {
+  auto compute = [&](int i, const WChunk<BITS>(&w)[2], const float(&sc)[2]) __attribute__((always_inline)) {
     if constexpr (FOLDED) {
-      compute_body(i, w, sc, tail_tag, std::true_type{});
+      compute_body(i, w, sc, std::true_type{});
     } else {
       if (__all(dq_fast_ok(sc[0]) && dq_fast_ok(sc[1])))
-        compute_body(i, w, sc, tail_tag, std::true_type{});
+        compute_body(i, w, sc, std::true_type{});
       else
-        compute_body(i, w, sc, tail_tag, std::false_type{});
+        compute_body(i, w, sc, std::false_type{});
     }
   };
 
@@ -382,13 +399,23 @@ __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, in
   WChunk<BITS> wb[kD][2];
   float sb[kD][2];
   u32x4 av[kD][NRT];
+  // The prologue is kD load-only steps -kD .. -1 issuing exactly what a
+  // steady step issues, in the same order (tokens j+1+kD, weights j+kD), so
+  // every load has the same number of younger loads behind it in the first
+  // loop iteration as in later ones: the compiler's wait counts (one per
+  // instruction, valid on every path into the loop) then never drain the
+  // prefetch.
+  // (sched_barrier keeps the machine scheduler from regrouping the loads.)
+  load_a(0, av[0]);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int d = 0; d < kD; ++d) {
-    load_a(d, av[d]);
-    load_w(d, wb[d], sb[d]);
+  for (int j = -kD; j < 0; ++j) {
+    if (j == -1) store_a(0, av[0]);
+    load_a(j + 1 + kD, av[(j + 1 + kD) % kD]);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(j + kD, wb[(j + kD) % kD], sb[(j + kD) % kD]);
+    __builtin_amdgcn_sched_barrier(0);
   }
-  store_a(0, av[0]);
-  load_a(kD, av[0]);
   __syncthreads();  // chunk 0 staged
 
   // One step per chunk, kD steps per loop iteration (static register slots).
@@ -397,13 +424,13 @@ __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, in
   auto step = [&](int i, auto d_tag) __attribute__((always_inline)) {
     constexpr int d = decltype(d_tag)::value;
     constexpr int dn = (d + 1) % kD;
-    if (i + 1 < nk || (i + 1 == nk && (K % kKC) == 0))
-      compute(i, wb[d], sb[d], std::false_type{});
-    else if (i + 1 == nk)
-      compute(i, wb[d], sb[d], std::true_type{});  // the partial last chunk
+    if (i < nk) compute(i, wb[d], sb[d]);
+    __builtin_amdgcn_sched_barrier(0);
     store_a(i + 1, av[dn]);
     load_a(i + 1 + kD, av[dn]);
+    __builtin_amdgcn_sched_barrier(0);
     load_w(i + kD, wb[d], sb[d]);
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();  // chunk i consumed by every wave, chunk i + 1 staged
   };
   for (int i0 = 0; i0 < nk; i0 += kD) {
@@ -449,13 +476,13 @@ __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, in
   }
 }
 
-template <int BITS, bool FOLDED, bool FIRST>
+template <int BITS, bool FOLDED, bool FIRST, bool G128>
 __device__ __forceinline__ void gemm_dispatch(const MoeArgs &a, int e, int slice, int row0, int rows,
                                               unsigned char *lds) {
   if (rows <= 16)
-    gemm_item<BITS, FOLDED, 1, FIRST>(a, e, slice, row0, rows, lds);
+    gemm_item<BITS, FOLDED, 1, FIRST, G128>(a, e, slice, row0, rows, lds);
   else
-    gemm_item<BITS, FOLDED, 2, FIRST>(a, e, slice, row0, rows, lds);
+    gemm_item<BITS, FOLDED, 2, FIRST, G128>(a, e, slice, row0, rows, lds);
 }
 
 // out[t, h..h+8) = bf16(sum_j y[t*k + j, h..h+8)) over the routed slots, j ascending
@@ -495,9 +522,10 @@ __global__ __launch_bounds__(kCombineBlock) void combine_kernel(const float *__r
 // the slices of one row block -- which stage the same token rows -- and the
 // row blocks of one expert -- which read the same weights at about the same
 // time -- meet in one L2.  Workgroups of an XCD take its items round-robin;
-// the grid is a multiple of 8.
-template <int BITS, bool FOLDED, bool FIRST>
-__global__ __launch_bounds__(kThreads, 2) void moe_gemm_kernel(MoeArgs a) {
+// the grid is a multiple of 8.  G128: the group length along K is 128 (the
+// scale of a chunk is its group), else any multiple of 32.
+template <int BITS, bool FOLDED, bool FIRST, bool G128>
+__global__ __launch_bounds__(kThreads, 3) void moe_gemm_kernel(MoeArgs a) {
   __shared__ __align__(16) unsigned char lds[kStages * kStageBytes];
   const int nb = __builtin_amdgcn_readfirstlane(a.hdr->n_blk);
   const int per = FIRST ? a.I / kF1 : a.H / kR2;
@@ -514,7 +542,7 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_kernel(MoeArgs a) {
     const int e = __builtin_amdgcn_readfirstlane(bi.x);
     const int row0 = __builtin_amdgcn_readfirstlane(bi.y);
     const int rows = __builtin_amdgcn_readfirstlane(bi.z);
-    gemm_dispatch<BITS, FOLDED, FIRST>(a, e, slice, row0, rows, lds);
+    gemm_dispatch<BITS, FOLDED, FIRST, G128>(a, e, slice, row0, rows, lds);
   }
 }
 
@@ -532,6 +560,8 @@ struct PlanArgs {
   int32_t *counts;
   int32_t *offsets;
   int32_t *sorted;
+  int32_t *srow;  // token of each sorted row (nullptr: not written)
+  int k;
   // block table (blocks == nullptr: permutation only)
   int4 *blocks;
   PlanHeader *hdr;
@@ -641,6 +671,7 @@ __global__ __launch_bounds__(kPlanBlock) void plan_kernel(PlanArgs p) {
       int pos = base[key] + rank;
       for (int w = 0; w < wave; ++w) pos += wcnt[w][key];
       p.sorted[pos] = static_cast<int32_t>(a);
+      if (p.srow) p.srow[pos] = static_cast<int32_t>(a / p.k);
     }
     __syncthreads();
     for (int e = tid; e < E; e += kPlanBlock) {
@@ -668,7 +699,7 @@ __global__ __launch_bounds__(256) void permute_rows_kernel(const uint16_t *__res
 // ---------------------------------------------------------------------------
 
 struct WsLayout {
-  size_t counts, offsets, sorted, hdr, blocks, ids, weights, xperm, act, ybuf, total;
+  size_t counts, offsets, sorted, srow, hdr, blocks, ids, weights, xperm, act, ybuf, total;
 };
 
 inline size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
@@ -690,6 +721,7 @@ WsLayout ws_layout(int64_t T, int H, int I, int E, int k) {
   take(w.counts, sizeof(int32_t) * E);
   take(w.offsets, sizeof(int32_t) * (E + 1));
   take(w.sorted, sizeof(int32_t) * N);
+  take(w.srow, sizeof(int32_t) * N);
   take(w.hdr, sizeof(PlanHeader));
   take(w.blocks, sizeof(int4) * max_blocks_for(T, E, k));
   take(w.ids, sizeof(int32_t) * N);
@@ -705,7 +737,7 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 // persistent grid: resident workgroups of one GEMM kernel on this device,
 // a multiple of 8 (one share per XCD), no more than the items can use
-template <int BITS, bool FOLDED, bool FIRST>
+template <int BITS, bool FOLDED, bool FIRST, bool G128>
 int gemm_grid(int64_t max_items) {
   static int cached[64] = {0};
   int dev = 0;
@@ -714,7 +746,7 @@ int gemm_grid(int64_t max_items) {
   if (g == 0) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, moe_gemm_kernel<BITS, FOLDED, FIRST>, kThreads, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, moe_gemm_kernel<BITS, FOLDED, FIRST, G128>, kThreads, 0) !=
             hipSuccess ||
         per_cu <= 0)
       per_cu = 1;
@@ -785,11 +817,18 @@ int validate_layer(const void *x, int64_t T, int H, int I, int E, int k, const i
 // G1 -> G2 -> combine, marks[first + 1 ..] after each
 template <int BITS, bool FOLDED>
 int launch_phases(const MoeArgs &a, int64_t max_g1, int64_t max_g2, hipStream_t st, ProfileMarks &pm, int first) {
-  moe_gemm_kernel<BITS, FOLDED, true><<<gemm_grid<BITS, FOLDED, true>(max_g1), kThreads, 0, st>>>(a);
+  if (a.g1 == kKC)
+    moe_gemm_kernel<BITS, FOLDED, true, true><<<gemm_grid<BITS, FOLDED, true, true>(max_g1), kThreads, 0, st>>>(a);
+  else
+    moe_gemm_kernel<BITS, FOLDED, true, false><<<gemm_grid<BITS, FOLDED, true, false>(max_g1), kThreads, 0, st>>>(a);
   int rc = check_launch("moe_gemm1");
   if (rc) return rc;
   pm.mark(first + 1);
-  moe_gemm_kernel<BITS, FOLDED, false><<<gemm_grid<BITS, FOLDED, false>(max_g2), kThreads, 0, st>>>(a);
+  if (a.g2 == kKC)
+    moe_gemm_kernel<BITS, FOLDED, false, true><<<gemm_grid<BITS, FOLDED, false, true>(max_g2), kThreads, 0, st>>>(a);
+  else
+    moe_gemm_kernel<BITS, FOLDED, false, false><<<gemm_grid<BITS, FOLDED, false, false>(max_g2), kThreads, 0, st>>>(
+        a);
   rc = check_launch("moe_gemm2");
   if (rc) return rc;
   pm.mark(first + 2);
@@ -823,6 +862,8 @@ int moe_forward_impl(const void *x, bool x_permuted, int64_t T, int H, int I, in
   p.offsets = reinterpret_cast<int32_t *>(ws + w.offsets);
   p.sorted = reinterpret_cast<int32_t *>(ws + w.sorted);
   p.blocks = reinterpret_cast<int4 *>(ws + w.blocks);
+  p.srow = reinterpret_cast<int32_t *>(ws + w.srow);
+  p.k = k;
   p.hdr = reinterpret_cast<PlanHeader *>(ws + w.hdr);
   uint16_t *xperm = reinterpret_cast<uint16_t *>(ws + w.xperm);
   if (!x_permuted) {
@@ -846,6 +887,7 @@ int moe_forward_impl(const void *x, bool x_permuted, int64_t T, int H, int I, in
   a.offsets = p.offsets;
   a.sorted = p.sorted;
   a.blocks = p.blocks;
+  a.srow = p.srow;
   a.hdr = p.hdr;
   a.act = reinterpret_cast<uint16_t *>(ws + w.act);
   a.ybuf = reinterpret_cast<float *>(ws + w.ybuf);
@@ -890,6 +932,8 @@ int launch_permute(const int32_t *ids, int64_t N, int E, int32_t *counts, int32_
   p.offsets = offsets;
   p.sorted = sorted;
   p.blocks = nullptr;
+  p.srow = nullptr;
+  p.k = 1;
   plan_kernel<<<1, kPlanBlock, 0, st>>>(p);
   return check_launch("moe_permute");
 }
