@@ -43,6 +43,7 @@
 // Both feed the same K order to A and B: within each 8-value MFMA slot the K
 // order is [0,4,1,5,2,6,3,7]; the staging wave permutes the token rows to
 // match.
+#include <mutex>
 #include <type_traits>
 
 #include "lq_common.h"
@@ -67,7 +68,7 @@ constexpr int kStageBytes = kRowsMax * kRowBytes;  // one LDS stage
 constexpr int kStages = 2;                      // LDS stages (double buffer)
 constexpr int kF1 = 64;                         // G1 features per item (128 weight rows)
 constexpr int kR2 = 128;                        // G2 output rows per item
-constexpr int kCombineBlock = 256;             // combine: 8 outputs per thread
+constexpr int kCombineBlock = 256;             // combine: 2 outputs per thread
 
 // 128-wide K chunks of weights in flight per wave: 8 KB per wave either way
 // (INT4: 2 tiles x 1 KB per chunk; INT8: 2 tiles x 2 KB)
@@ -82,6 +83,7 @@ struct alignas(16) PlanHeader {
 };
 
 struct MoeArgs {
+  const uint16_t *x;       // [T, H] bf16
   const uint16_t *xperm;   // [T, H] bf16, K slots permuted (kslot)
   const int8_t *q1;        // [E, 2I, H] int8 or [E, 2I, H/2] packed
   const float *s1;         // [E, 2I, ng1]
@@ -185,6 +187,78 @@ template <>
 struct WChunk<8> {
   uint4 v0, v1;
 };
+
+// One 128-wide K chunk: dequantize this lane's codes of NT 16-row weight
+// tiles into B fragments and multiply them with NRT 16-row tiles of token
+// rows staged in LDS at `buf` (row r at buf + r * 256, its 16-byte pieces
+// XOR-swizzled by r & 15).  FAST: every lane's scales pass dq_fast_ok
+// (wave-uniform choice).  In the partial last chunk of a K that is not a
+// multiple of 128, lanes past K hold zero codes (out-of-range loads), which
+// dequantize to +0 and meet finite token values; the folded form never sees
+// such a chunk (it needs group lengths that are multiples of 128).
+template <int BITS, bool FOLDED, bool FAST, int NRT, int NT>
+__device__ __forceinline__ void chunk_mfma(const WChunk<BITS> (&w)[NT], const float (&sc)[NT],
+                                           const unsigned char *buf, int lc, int lg, floatx4 (&tot)[NRT][NT]) {
+  const uint4 ones4 = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);  // bf16 1.0
+  floatx4 acc[NRT][NT];
+  floatx4 xs[NRT];
+  DqScale dqs[NT];
+#pragma unroll
+  for (int c = 0; c < NT; ++c) dqs[c] = dq_scale<BITS>(sc[c]);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    uint4 b[NT];
+#pragma unroll
+    for (int c = 0; c < NT; ++c) {
+      if constexpr (BITS == 4) {
+        const uint32_t q = s == 0 ? w[c].v.x : s == 1 ? w[c].v.y : s == 2 ? w[c].v.z : w[c].v.w;
+        if constexpr (FOLDED)
+          b[c] = b_int4_folded(q);
+        else
+          b[c] = b_int4_exact<FAST>(q, sc[c], dqs[c]);
+      } else {
+        const uint4 &v = s < 2 ? w[c].v0 : w[c].v1;
+        const uint32_t d0 = (s & 1) ? v.z : v.x;
+        const uint32_t d1 = (s & 1) ? v.w : v.y;
+        if constexpr (FOLDED)
+          b[c] = b_int8_folded(d0, d1);
+        else
+          b[c] = b_int8_exact<FAST>(d0, d1, sc[c], dqs[c]);
+      }
+    }
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) {
+      // row rt*16 + lc (its low 4 bits are lc), K piece 4*lg + s of this 128-wide chunk
+      const uint4 af = *reinterpret_cast<const uint4 *>(buf + (rt * 16 + lc) * kRowBytes +
+                                                        16 * ((4 * lg + s) ^ lc));
+      if constexpr (!FOLDED) {
+#pragma unroll
+        for (int c = 0; c < NT; ++c)
+          tot[rt][c] =
+              __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(af), as_bf16x8(b[c]), tot[rt][c], 0, 0, 0);
+      } else {
+        const floatx4 z = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < NT; ++c)
+          acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(af), as_bf16x8(b[c]),
+                                                               s == 0 ? z : acc[rt][c], 0, 0, 0);
+        xs[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(af), as_bf16x8(ones4), s == 0 ? z : xs[rt],
+                                                         0, 0, 0);
+      }
+    }
+  }
+  if constexpr (FOLDED) {
+    // sum x*q = S - bias * X, then the column's group scale
+    constexpr float kBias = BITS == 4 ? 136.0f : 128.0f;
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+      for (int c = 0; c < NT; ++c)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          tot[rt][c][j] = fmaf(sc[c], fmaf(-kBias, xs[rt][j], acc[rt][c][j]), tot[rt][c][j]);
+  }
+}
 
 // ---------------------------------------------------------------------------
 // one G1 / G2 item
@@ -306,84 +380,15 @@ __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, in
 #pragma unroll
     for (int c = 0; c < 2; ++c) tot[rt][c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // one 128-wide K chunk of this wave's two tiles against the staged rows.
-  // FAST: every lane's scales pass dq_fast_ok (wave-uniform choice).  In
-  // the partial last chunk of a K that is not a multiple of 128, lanes past
-  // K loaded zero codes (out of range), which dequantize to +0 and meet
-  // finite token values; the folded form never sees such a chunk (it needs
-  // group lengths that are multiples of 128, hence K % 128 == 0).
-  auto compute_body = [&](int i, const WChunk<BITS>(&w)[2], const float(&sc)[2], auto fast_tag)
-      __attribute__((always_inline)) {
-    constexpr bool FAST = decltype(fast_tag)::value;
-    const unsigned char *buf = lds + (i % kStages) * kStageBytes;
-    const uint4 ones4 = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);  // bf16 1.0
-    floatx4 acc[NRT][2];
-    floatx4 xs[NRT];
-    DqScale dqs[2];
-#pragma unroll
-    for (int c = 0; c < 2; ++c) dqs[c] = dq_scale<BITS>(sc[c]);
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      uint4 b[2];
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        if constexpr (BITS == 4) {
-          const uint32_t q = s == 0 ? w[c].v.x : s == 1 ? w[c].v.y : s == 2 ? w[c].v.z : w[c].v.w;
-          if constexpr (FOLDED)
-            b[c] = b_int4_folded(q);
-          else
-            b[c] = b_int4_exact<FAST>(q, sc[c], dqs[c]);
-        } else {
-          const uint4 &v = s < 2 ? w[c].v0 : w[c].v1;
-          const uint32_t d0 = (s & 1) ? v.z : v.x;
-          const uint32_t d1 = (s & 1) ? v.w : v.y;
-          if constexpr (FOLDED)
-            b[c] = b_int8_folded(d0, d1);
-          else
-            b[c] = b_int8_exact<FAST>(d0, d1, sc[c], dqs[c]);
-        }
-      }
-#pragma unroll
-      for (int rt = 0; rt < NRT; ++rt) {
-        // row rt*16 + lc (its low 4 bits are lc), K piece 4*lg + s of this 128-wide chunk
-        const uint4 af = *reinterpret_cast<const uint4 *>(buf + (rt * 16 + lc) * kRowBytes +
-                                                          16 * ((4 * lg + s) ^ lc));
-        if constexpr (!FOLDED) {
-#pragma unroll
-          for (int c = 0; c < 2; ++c)
-            tot[rt][c] =
-                __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(af), as_bf16x8(b[c]), tot[rt][c], 0, 0, 0);
-        } else {
-          const floatx4 z = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-          for (int c = 0; c < 2; ++c)
-            acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(af), as_bf16x8(b[c]),
-                                                                 s == 0 ? z : acc[rt][c], 0, 0, 0);
-          xs[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(af), as_bf16x8(ones4), s == 0 ? z : xs[rt],
-                                                           0, 0, 0);
-        }
-      }
-    }
-    if constexpr (FOLDED) {
-      // sum x*q = S - bias * X, then the column's group scale
-      constexpr float kBias = BITS == 4 ? 136.0f : 128.0f;
-#pragma unroll
-      for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            tot[rt][c][j] = fmaf(sc[c], fmaf(-kBias, xs[rt][j], acc[rt][c][j]), tot[rt][c][j]);
-    }
-  };
   auto compute = [&](int i, const WChunk<BITS>(&w)[2], const float(&sc)[2]) __attribute__((always_inline)) {
+    const unsigned char *buf = lds + (i % kStages) * kStageBytes;
     if constexpr (FOLDED) {
-      compute_body(i, w, sc, std::true_type{});
+      chunk_mfma<BITS, FOLDED, true, NRT, 2>(w, sc, buf, lc, lg, tot);
     } else {
       if (__all(dq_fast_ok(sc[0]) && dq_fast_ok(sc[1])))
-        compute_body(i, w, sc, std::true_type{});
+        chunk_mfma<BITS, FOLDED, true, NRT, 2>(w, sc, buf, lc, lg, tot);
       else
-        compute_body(i, w, sc, std::false_type{});
+        chunk_mfma<BITS, FOLDED, false, NRT, 2>(w, sc, buf, lc, lg, tot);
     }
   };
 
@@ -485,35 +490,25 @@ __device__ __forceinline__ void gemm_dispatch(const MoeArgs &a, int e, int slice
     gemm_item<BITS, FOLDED, 2, FIRST, G128>(a, e, slice, row0, rows, lds);
 }
 
-// out[t, h..h+8) = bf16(sum_j y[t*k + j, h..h+8)) over the routed slots, j ascending
+// out[t, h..h+2) = bf16(sum_j y[t*k + j, h..h+2)) over the routed slots, j
+// ascending (2 outputs per thread: enough threads to cover every CU)
 __global__ __launch_bounds__(kCombineBlock) void combine_kernel(const float *__restrict__ ybuf,
                                                                 const int32_t *__restrict__ ids, int64_t T,
                                                                 int H, int k, int E, uint16_t *__restrict__ out) {
-  const int64_t base = (static_cast<int64_t>(blockIdx.x) * kCombineBlock + threadIdx.x) * 8;
+  const int64_t base = (static_cast<int64_t>(blockIdx.x) * kCombineBlock + threadIdx.x) * 2;
   if (base >= T * H) return;
   const int64_t t = base / H;
   const int h = static_cast<int>(base - t * H);
-  float s[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  float s0 = 0.0f, s1 = 0.0f;
   for (int j = 0; j < k; ++j) {
     const int id = ids[t * k + j];
     if (id < 0 || id >= E) continue;
-    const float4 *y = reinterpret_cast<const float4 *>(ybuf + (t * k + j) * H + h);
-    const float4 v0 = y[0], v1 = y[1];
-    s[0] += v0.x;
-    s[1] += v0.y;
-    s[2] += v0.z;
-    s[3] += v0.w;
-    s[4] += v1.x;
-    s[5] += v1.y;
-    s[6] += v1.z;
-    s[7] += v1.w;
+    const float2 v = *reinterpret_cast<const float2 *>(ybuf + (t * k + j) * H + h);
+    s0 += v.x;
+    s1 += v.y;
   }
-  uint32_t p[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    p[i] = static_cast<uint32_t>(f32_to_bf16_bits(s[2 * i])) |
-           (static_cast<uint32_t>(f32_to_bf16_bits(s[2 * i + 1])) << 16);
-  *reinterpret_cast<uint4 *>(out + base) = make_uint4(p[0], p[1], p[2], p[3]);
+  *reinterpret_cast<uint32_t *>(out + base) =
+      static_cast<uint32_t>(f32_to_bf16_bits(s0)) | (static_cast<uint32_t>(f32_to_bf16_bits(s1)) << 16);
 }
 
 // Persistent G1 (FIRST) or G2 kernel.  Items are (row block, slice) pairs,
@@ -543,6 +538,301 @@ __global__ __launch_bounds__(kThreads, 3) void moe_gemm_kernel(MoeArgs a) {
     const int row0 = __builtin_amdgcn_readfirstlane(bi.y);
     const int rows = __builtin_amdgcn_readfirstlane(bi.z);
     gemm_dispatch<BITS, FOLDED, FIRST, G128>(a, e, slice, row0, rows, lds);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// streaming G1 / G2 kernels (the weight-bandwidth regime)
+//
+// One 12-wave workgroup per CU (3 waves per SIMD).  A unit is one 16-row
+// weight tile of one row block over the whole K: G1 has 2I / 16 units per
+// block (gate rows, then up rows), G2 H / 16.  With no more blocks than
+// CUs, every block gets floor or ceil(CUs / blocks) CUs and each of them a
+// contiguous, equal share of the block's units, so every CU stages one block
+// and streams the same number of weight bytes (+-1 tile); with more blocks
+// than CUs each CU takes a contiguous range of whole blocks.  For each block
+// it handles, a CU stages the block's token rows for the whole K into LDS
+// once (up to 32 rows x K bf16 = K * 64 bytes, in 128-wide chunks laid out
+// as gemm_item's per-stage tiles); its waves then take the units round-robin
+// and stream each as one flat sequence of 128-wide K chunks with kD chunks
+// of codes and scales in flight and no barriers.
+//
+// G1 stores bf16(x . w) of each tile -- the gate and up pre-activations,
+// rounded as the reference rounds them -- into gu [T*k, 2I] (sorted rows);
+// G2's staging applies SwiGLU while it copies the rows into LDS, so gate
+// and up tiles need not meet in one wave.
+// ---------------------------------------------------------------------------
+
+constexpr int kSWaves = 12;
+constexpr int kSThreads = 64 * kSWaves;
+
+// LDS bytes of the streaming kernels for reduction length K (token rows of
+// one block for the whole K)
+inline size_t stream_lds_bytes(int K) { return static_cast<size_t>(K) * kRowsMax * 2; }
+
+// reference op order (INFERENCE_REPO_CHANGES.md:296-309): g, u -> bf16;
+// silu in fp32 -> bf16; bf16 product
+__device__ __forceinline__ uint16_t swiglu_bf16(float g, float u) {
+  const float gb = bf16_round(g);
+  const float ub = bf16_round(u);
+  const float sb16 = bf16_round(gb / (1.0f + __expf(-gb)));
+  return f32_to_bf16_bits(sb16 * ub);
+}
+
+// Token rows [row0, row0 + rows) of one block, whole K, into LDS chunk tiles.
+// G1 copies x into K-slot order; G2 builds act = SwiGLU(g, u) from
+// the gate / up pre-activations and permutes it into K-slot order.
+template <bool FIRST>
+__device__ __forceinline__ void stage_block(const MoeArgs &a, int row0, int rows, unsigned char *lds) {
+  const int K = FIRST ? a.H : a.I;
+  const int nk = K / kKC;
+  const int per_row = nk * 16;  // 16-byte pieces (8 values) per row
+  const int total = rows * per_row;
+  constexpr int kBatch = FIRST ? 8 : 4;
+  for (int q0 = 0; q0 < total; q0 += kBatch * kSThreads) {
+    u32x4 v[kBatch];
+    u32x4 vu[FIRST ? 1 : kBatch];
+    int dst[kBatch];
+    // every load is issued (pieces past the end re-read the last piece), so
+    // the batch is in flight at once; only the LDS stores are guarded
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int q0i = q0 + i * kSThreads + static_cast<int>(threadIdx.x);
+      const int q = q0i < total ? q0i : total - 1;
+      const int r = q / per_row;
+      const int rem = q - r * per_row;
+      const int c = rem >> 4, pc = rem & 15;
+      if constexpr (FIRST) {
+        const int64_t src = static_cast<int64_t>(a.srow[row0 + r]) * a.H + c * kKC + pc * 8;
+        v[i] = *reinterpret_cast<const u32x4 *>(a.x + src);
+      } else {
+        const int64_t src = static_cast<int64_t>(row0 + r) * (2 * a.I) + c * kKC + pc * 8;
+        v[i] = *reinterpret_cast<const u32x4 *>(a.act + src);           // gate, 8 features
+        vu[i] = *reinterpret_cast<const u32x4 *>(a.act + src + a.I);    // up, same features
+      }
+      dst[i] = q0i < total ? (c * kRowsMax + r) * kRowBytes + 16 * (pc ^ (r & 15)) : -1;
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      u32x4 o = v[i];
+      if constexpr (FIRST) {
+        const uint4 perm = permute_kslots(make_uint4(o[0], o[1], o[2], o[3]));  // x into K-slot order
+        o = u32x4{perm.x, perm.y, perm.z, perm.w};
+      } else {
+        uint32_t p[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const uint32_t gw = v[i][h], uw = vu[i][h];
+          const uint16_t lo = swiglu_bf16(__uint_as_float(gw << 16), __uint_as_float(uw << 16));
+          const uint16_t hi = swiglu_bf16(__uint_as_float(gw & 0xFFFF0000u), __uint_as_float(uw & 0xFFFF0000u));
+          p[h] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+        }
+        const uint4 perm = permute_kslots(make_uint4(p[0], p[1], p[2], p[3]));
+        o = u32x4{perm.x, perm.y, perm.z, perm.w};
+      }
+      if (dst[i] >= 0) *reinterpret_cast<u32x4 *>(lds + dst[i]) = o;
+    }
+  }
+}
+
+template <int BITS, bool FOLDED, bool FIRST, int NRT, int KD, bool SQ>
+__device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, int rows, int u_first, int u_end,
+                                             const unsigned char *lds) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int lc = lane & 15;
+  const int lg = lane >> 4;
+  const int f0 = u_first + wave;
+  const int nunits = f0 < u_end ? (u_end - f0 + kSWaves - 1) / kSWaves : 0;
+  const int K = FIRST ? a.H : a.I;
+  const int nk = K / kKC;  // a multiple of KD (host-checked)
+  const int nsteps = nunits * nk;
+  const int rowbytes = BITS == 4 ? (K >> 1) : K;
+  const int ng = FIRST ? a.ng1 : a.ng2;
+  const int cpg = (FIRST ? a.g1 : a.g2) / kKC;  // chunks per group (group lengths are multiples of 128)
+  const int nrows_w = FIRST ? 2 * a.I : a.H;
+  constexpr int kLaneBytes = BITS == 4 ? 16 : 32;
+  constexpr int kChunkBytes = BITS == 4 ? 64 : 128;
+  const __amdgpu_buffer_rsrc_t wrsrc =
+      make_rsrc((FIRST ? a.q1 : a.q2) + static_cast<int64_t>(e) * nrows_w * rowbytes,
+                static_cast<int64_t>(nrows_w) * rowbytes);
+  const __amdgpu_buffer_rsrc_t srsrc = make_rsrc((FIRST ? a.s1 : a.s2) + static_cast<int64_t>(e) * nrows_w * ng,
+                                                 static_cast<int64_t>(nrows_w) * ng * 4);
+  const __amdgpu_buffer_rsrc_t empty = make_rsrc(a.out, 0);
+  const int wvoff = lc * rowbytes + kLaneBytes * lg;  // this lane's codes within a tile chunk
+  const int svoff = lc * ng * 4;
+
+  // load cursor (scalar registers, advanced incrementally): the codes and
+  // scale offsets of the next chunk to load, its chunk index within the unit
+  // and the loads left; after the wave's last chunk both descriptors become
+  // the empty one.
+  // SQ (group length 128, at most 16 chunks): instead of one scale load per
+  // chunk, lane (r, g) loads the scales of groups 4g .. 4g+3 of its tile row
+  // r once per unit (one dwordx4, issued in the first step of every run of
+  // KD loads -- from the empty descriptor when that run does not start a
+  // unit); the scale of chunk c then comes from lane (r, c / 4) by
+  // ds_bpermute.
+  __amdgpu_buffer_rsrc_t rw = nsteps > 0 ? wrsrc : empty, rs = nsteps > 0 ? srsrc : empty;
+  int lu = f0;                                  // unit of the next load
+  int lcur = 0, lgrp = 0;                       // its chunk, and chunk within the group
+  int wso = 16 * lu * rowbytes;                 // codes offset of that chunk
+  int sso = 16 * lu * ng * 4;                   // scale offset of that chunk's group
+  int left = nsteps;
+  u32x4 sq_cur = u32x4{0, 0, 0, 0}, sq_next = u32x4{0, 0, 0, 0};
+  const int sqvoff = lc * ng * 4 + 16 * lg;     // SQ: this lane's 4 scales within a tile
+  auto load_sq = [&](u32x4 &dst) __attribute__((always_inline)) {
+    dst = __builtin_amdgcn_raw_buffer_load_b128(lcur == 0 ? rs : empty, sqvoff, lcur == 0 ? sso : 0, 0);
+  };
+  auto load_w = [&](WChunk<BITS>(&w)[1], float(&sc)[1]) __attribute__((always_inline)) {
+    if constexpr (BITS == 4) {
+      w[0].v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, wvoff, wso, 0));
+    } else {
+      w[0].v0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, wvoff, wso, 0));
+      w[0].v1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, wvoff + 16, wso, 0));
+    }
+    if constexpr (!SQ) sc[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, svoff, sso, 0));
+    wso += kChunkBytes;
+    if (++lgrp == cpg) {
+      lgrp = 0;
+      sso += 4;
+    }
+    if (++lcur == nk) {
+      lcur = 0;
+      lgrp = 0;
+      lu += kSWaves;
+      wso = 16 * lu * rowbytes;
+      sso = 16 * lu * ng * 4;
+    }
+    if (--left == 0) {
+      rw = empty;
+      rs = empty;
+      wso = 0;
+      sso = 0;
+    }
+  };
+
+  floatx4 tot[NRT][1];
+#pragma unroll
+  for (int rt = 0; rt < NRT; ++rt) tot[rt][0] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto epilogue = [&](int u) __attribute__((always_inline)) {
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int m = rt * 16 + 4 * lg + j;
+        if (m < rows) {
+          if constexpr (FIRST) {
+            // gate (u < I / 16) or up pre-activation, rounded to bf16
+            a.act[static_cast<int64_t>(row0 + m) * (2 * a.I) + 16 * u + lc] = f32_to_bf16_bits(tot[rt][0][j]);
+          } else {
+            const int asg = a.sorted[row0 + m];
+            a.ybuf[static_cast<int64_t>(asg) * a.H + 16 * u + lc] = tot[rt][0][j] * a.topk_w[asg];
+          }
+        }
+      }
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) tot[rt][0] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  };
+
+  // KD steps of codes in flight; step i consumes slot i % KD and refills it
+  // with step i + KD (loads past the wave's last step go through the empty
+  // descriptor, so every step issues the same loads)
+  WChunk<BITS> wb[KD][1];
+  float sb[KD][1];
+#pragma unroll
+  for (int d = 0; d < KD; ++d) {
+    if constexpr (SQ) {
+      if (d == 0) load_sq(sq_cur);
+    }
+    load_w(wb[d], sb[d]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // the block's token rows are staged while the first codes are in flight
+  __syncthreads();  // the previous block's rows are no longer read
+  stage_block<FIRST>(a, row0, rows, const_cast<unsigned char *>(lds));
+  __syncthreads();
+  if (nsteps == 0) return;
+  int cu = f0, cc = 0;  // compute cursor: unit, first chunk of the current KD steps
+  auto step = [&](auto d_tag) __attribute__((always_inline)) {
+    constexpr int d = decltype(d_tag)::value;
+    const unsigned char *buf = lds + (cc + d) * (kRowsMax * kRowBytes);
+    if constexpr (SQ) {
+      // chunk cc + d (cc is a multiple of 4): component d % 4 of lane (r, (cc + d) / 4)
+      const int src = (lc + 16 * ((cc + d) >> 2)) << 2;
+      sb[d][0] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(sq_cur[d & 3])));
+    }
+    if constexpr (FOLDED) {
+      chunk_mfma<BITS, FOLDED, true, NRT, 1>(wb[d], sb[d], buf, lc, lg, tot);
+    } else {
+      if (__all(dq_fast_ok(sb[d][0])))
+        chunk_mfma<BITS, FOLDED, true, NRT, 1>(wb[d], sb[d], buf, lc, lg, tot);
+      else
+        chunk_mfma<BITS, FOLDED, false, NRT, 1>(wb[d], sb[d], buf, lc, lg, tot);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (SQ) {
+      if (d == 0) load_sq(sq_next);
+    }
+    load_w(wb[d], sb[d]);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // nk is a multiple of KD, so a unit ends only after the last step of a block
+  for (int s0 = 0; s0 < nsteps; s0 += KD) {
+    step(std::integral_constant<int, 0>{});
+    step(std::integral_constant<int, 1>{});
+    if constexpr (KD > 2) {
+      step(std::integral_constant<int, 2>{});
+      step(std::integral_constant<int, 3>{});
+    }
+    if constexpr (KD > 4) {
+      step(std::integral_constant<int, 4>{});
+      step(std::integral_constant<int, 5>{});
+      step(std::integral_constant<int, 6>{});
+      step(std::integral_constant<int, 7>{});
+    }
+    cc += KD;
+    if (cc == nk) {
+      epilogue(cu);
+      cc = 0;
+      cu += kSWaves;
+      if constexpr (SQ) sq_cur = sq_next;
+    }
+  }
+}
+
+template <int BITS, bool FOLDED, bool FIRST, int KD, bool SQ>
+__device__ __forceinline__ void stream_block(const MoeArgs &a, int blk, int u_first, int u_end,
+                                             unsigned char *lds) {
+  const int4 bi = a.blocks[blk];
+  const int e = __builtin_amdgcn_readfirstlane(bi.x);
+  const int row0 = __builtin_amdgcn_readfirstlane(bi.y);
+  const int rows = __builtin_amdgcn_readfirstlane(bi.z);
+  if (rows <= 16)
+    stream_units<BITS, FOLDED, FIRST, 1, KD, SQ>(a, e, row0, rows, u_first, u_end, lds);
+  else
+    stream_units<BITS, FOLDED, FIRST, 2, KD, SQ>(a, e, row0, rows, u_first, u_end, lds);
+}
+
+template <int BITS, bool FOLDED, bool FIRST, int KD, bool SQ>
+__global__ __launch_bounds__(kSThreads, 1) void moe_stream_kernel(MoeArgs a) {
+  extern __shared__ __align__(16) unsigned char slds[];
+  const int upb = FIRST ? 2 * a.I / 16 : a.H / 16;  // units (16-row tiles) per row block
+  const int nb = __builtin_amdgcn_readfirstlane(a.hdr->n_blk);
+  const int G = gridDim.x, c = blockIdx.x;
+  if (nb <= G) {
+    // CUs [ceil(b G / nb), ceil((b+1) G / nb)) share block b
+    const int b = static_cast<int>(static_cast<int64_t>(c) * nb / G);
+    if (b >= nb) return;
+    const int first = static_cast<int>((static_cast<int64_t>(b) * G + nb - 1) / nb);
+    const int next = static_cast<int>((static_cast<int64_t>(b + 1) * G + nb - 1) / nb);
+    const int m = next - first, i = c - first;
+    const int ub = i * upb / m, ue = (i + 1) * upb / m;
+    stream_block<BITS, FOLDED, FIRST, KD, SQ>(a, b, ub, ue, slds);
+  } else {
+    const int b0 = static_cast<int>(static_cast<int64_t>(c) * nb / G);
+    const int b1 = static_cast<int>(static_cast<int64_t>(c + 1) * nb / G);
+    for (int b = b0; b < b1; ++b) stream_block<BITS, FOLDED, FIRST, KD, SQ>(a, b, 0, upb, slds);
   }
 }
 
@@ -595,7 +885,10 @@ __device__ void wave0_exclusive_scan(const int *in, int *out, int E, int *total)
   if (lane == 0) *total = tot;
 }
 
-__global__ __launch_bounds__(kPlanBlock) void plan_kernel(PlanArgs p) {
+// the plan for one workgroup of kPlanBlock threads; id_at(a) returns the
+// expert of assignment a (read from memory or from LDS)
+template <class IdAt>
+__device__ __forceinline__ void plan_body(const PlanArgs &p, IdAt id_at) {
   __shared__ int hist[kMaxExperts];
   __shared__ int base[kMaxExperts];
   __shared__ int nbs[kMaxExperts + 1];  // exclusive scan of row blocks per expert
@@ -609,7 +902,7 @@ __global__ __launch_bounds__(kPlanBlock) void plan_kernel(PlanArgs p) {
   for (int i = tid; i < kPlanWaves * kMaxExperts; i += kPlanBlock) (&wcnt[0][0])[i] = 0;
   __syncthreads();
   for (int64_t a = tid; a < p.N; a += kPlanBlock) {
-    const int id = p.ids[a];
+    const int id = id_at(a);
     if (id >= 0 && id < E) atomicAdd(&hist[id], 1);
   }
   __syncthreads();
@@ -655,7 +948,7 @@ __global__ __launch_bounds__(kPlanBlock) void plan_kernel(PlanArgs p) {
   const unsigned long long lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   for (int64_t chunk = 0; chunk < p.N; chunk += kPlanBlock) {
     const int64_t a = chunk + tid;
-    const int raw = a < p.N ? p.ids[a] : -1;
+    const int raw = a < p.N ? id_at(a) : -1;
     const bool valid = raw >= 0 && raw < E;
     const int key = valid ? raw : E;
     unsigned long long peers = ~0ull;
@@ -684,6 +977,25 @@ __global__ __launch_bounds__(kPlanBlock) void plan_kernel(PlanArgs p) {
     }
     __syncthreads();
   }
+}
+
+__global__ __launch_bounds__(kPlanBlock) void plan_kernel(PlanArgs p) {
+  plan_body(p, [&](int64_t a) { return p.ids[a]; });
+}
+
+// Front end of a small layer in one workgroup: the router (one wave per
+// token, route_token) writes ids and weights and keeps the ids in LDS, then
+// the plan runs on them -- one launch instead of two.
+constexpr int kFrontMaxN = 2048;  // assignments T * k the front kernel takes
+template <int LDT, int EPL>
+__global__ __launch_bounds__(kPlanBlock) void front_kernel(PlanArgs p, const void *logits, int64_t T, int k,
+                                                          int renorm, float *weights) {
+  __shared__ int32_t ids_lds[kFrontMaxN];
+  const int wave = threadIdx.x >> 6;
+  for (int64_t t = wave; t < T; t += kPlanWaves)
+    route_token<LDT, EPL>(logits, t, p.E, k, renorm, const_cast<int32_t *>(p.ids), weights, ids_lds);
+  __syncthreads();
+  plan_body(p, [&](int64_t a) { return ids_lds[a]; });
 }
 
 // x [rows, H] -> xperm, each group of 8 bf16 in K-slot order (8 values per thread)
@@ -727,7 +1039,7 @@ WsLayout ws_layout(int64_t T, int H, int I, int E, int k) {
   take(w.ids, sizeof(int32_t) * N);
   take(w.weights, sizeof(float) * N);
   take(w.xperm, sizeof(uint16_t) * T * H);
-  take(w.act, sizeof(uint16_t) * N * I);
+  take(w.act, sizeof(uint16_t) * N * 2 * I);  // act [N, I] (general) or gate/up [N, 2I] (streaming)
   take(w.ybuf, sizeof(float) * N * H);
   w.total = off;
   return w;
@@ -784,7 +1096,7 @@ int validate_layer(const void *x, int64_t T, int H, int I, int E, int k, const i
   if (E < 1 || E > kMaxExperts)
     return fail(LQ_ERR_UNSUPPORTED, "moe_forward: 1 <= num_experts <= " + std::to_string(kMaxExperts));
   if (k > E) return fail(LQ_ERR_VALUE, "moe_forward: top_k exceeds num_experts");
-  if (flags & ~LQ_MOE_FOLDED_SCALES) return fail(LQ_ERR_VALUE, "moe_forward: unknown flags");
+  if (flags & ~(LQ_MOE_FOLDED_SCALES | LQ_MOE_GENERAL_KERNEL)) return fail(LQ_ERR_VALUE, "moe_forward: unknown flags");
   if (H % kR2 != 0 || I % kF1 != 0)
     return fail(LQ_ERR_UNSUPPORTED, "moe_forward: needs hidden % 128 == 0 and intermediate % 64 == 0");
   const int64_t g1 = effective_group(H, group_w1);
@@ -815,8 +1127,74 @@ int validate_layer(const void *x, int64_t T, int H, int I, int E, int k, const i
 }
 
 // G1 -> G2 -> combine, marks[first + 1 ..] after each
+// per-device facts the launches need (queried once per device)
+struct DeviceInfo {
+  int cus = 0;         // compute units
+  int max_lds = 0;     // LDS bytes one workgroup may use
+};
+DeviceInfo device_info() {
+  static DeviceInfo cache[64];
+  static std::once_flag once[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  std::call_once(once[dev], [dev] {
+    DeviceInfo d;
+    if (hipDeviceGetAttribute(&d.cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || d.cus <= 0)
+      d.cus = 256;
+    if (hipDeviceGetAttribute(&d.max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+      d.max_lds = 65536;
+    cache[dev] = d;
+  });
+  return cache[dev];
+}
+
+// The streaming kernels cover shapes whose K splits into whole runs of 4
+// (INT4) or 2 (INT8) 128-wide chunks -- the chunks of codes kept in flight
+// -- with group lengths that are multiples of 128, and whose token rows for
+// the whole K fit one workgroup's LDS.
+bool stream_eligible(int bits, int H, int I, int64_t g1, int64_t g2) {
+  const int step = kKC * (bits == 4 ? 4 : 2);
+  const size_t lds = stream_lds_bytes(std::max(H, I));
+  return H % step == 0 && I % step == 0 && g1 % kKC == 0 && g2 % kKC == 0 &&
+         lds <= static_cast<size_t>(device_info().max_lds);
+}
+
+template <int BITS, bool FOLDED, bool FIRST, int KD, bool SQ>
+int launch_stream_kd(const MoeArgs &a, hipStream_t st) {
+  const DeviceInfo dev = device_info();
+  static std::once_flag attr_once;
+  static hipError_t attr_rc = hipSuccess;
+  std::call_once(attr_once, [&] {
+    attr_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(moe_stream_kernel<BITS, FOLDED, FIRST, KD, SQ>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, dev.max_lds);
+  });
+  if (attr_rc != hipSuccess)
+    return fail(LQ_ERR_RUNTIME, std::string("hipFuncSetAttribute failed: ") + hipGetErrorString(attr_rc));
+  const size_t lds = stream_lds_bytes(FIRST ? a.H : a.I);
+  moe_stream_kernel<BITS, FOLDED, FIRST, KD, SQ><<<dev.cus, kSThreads, lds, st>>>(a);
+  return check_launch(FIRST ? "moe_stream_gemm1" : "moe_stream_gemm2");
+}
+
+// chunks in flight per wave: 8 KB of codes where K allows (INT4: 8 x 1 KB,
+// INT8: 4 x 2 KB), half that otherwise; the folded INT4 form keeps 4 (its
+// extra accumulators leave no registers for 8)
+template <int BITS, bool FOLDED, bool FIRST>
+int launch_stream(const MoeArgs &a, hipStream_t st) {
+  const int nk = (FIRST ? a.H : a.I) / kKC;
+  constexpr int kDeep = BITS == 4 ? (FOLDED ? 4 : 8) : 4;
+  // per-unit scale loads: group length 128, at most 16 groups, runs of 4
+  const bool sq = (FIRST ? a.g1 : a.g2) == kKC && nk <= 16;
+  if (nk % kDeep == 0)
+    return sq ? launch_stream_kd<BITS, FOLDED, FIRST, kDeep, true>(a, st)
+              : launch_stream_kd<BITS, FOLDED, FIRST, kDeep, false>(a, st);
+  if constexpr (kDeep / 2 >= 4) {
+    if (sq) return launch_stream_kd<BITS, FOLDED, FIRST, kDeep / 2, true>(a, st);
+  }
+  return launch_stream_kd<BITS, FOLDED, FIRST, kDeep / 2, false>(a, st);
+}
+
 template <int BITS, bool FOLDED>
-int launch_phases(const MoeArgs &a, int64_t max_g1, int64_t max_g2, hipStream_t st, ProfileMarks &pm, int first) {
+int launch_general(const MoeArgs &a, int64_t max_g1, int64_t max_g2, hipStream_t st, ProfileMarks &pm, int first) {
   if (a.g1 == kKC)
     moe_gemm_kernel<BITS, FOLDED, true, true><<<gemm_grid<BITS, FOLDED, true, true>(max_g1), kThreads, 0, st>>>(a);
   else
@@ -832,31 +1210,38 @@ int launch_phases(const MoeArgs &a, int64_t max_g1, int64_t max_g2, hipStream_t 
   rc = check_launch("moe_gemm2");
   if (rc) return rc;
   pm.mark(first + 2);
-  const int64_t n8 = a.T * a.H / 8;
-  combine_kernel<<<static_cast<int>(ceil_div(n8, kCombineBlock)), kCombineBlock, 0, st>>>(a.ybuf, a.ids, a.T, a.H,
+  return LQ_OK;
+}
+
+template <int BITS, bool FOLDED>
+int launch_phases(const MoeArgs &a, int64_t max_g1, int64_t max_g2, hipStream_t st, ProfileMarks &pm, int first,
+                  bool stream) {
+  if (stream) {
+    int rc = launch_stream<BITS, FOLDED, true>(a, st);
+    if (rc) return rc;
+    pm.mark(first + 1);
+    rc = launch_stream<BITS, FOLDED, false>(a, st);
+    if (rc) return rc;
+    pm.mark(first + 2);
+  } else {
+    int rc = launch_general<BITS, FOLDED>(a, max_g1, max_g2, st, pm, first);
+    if (rc) return rc;
+  }
+  const int64_t n2 = a.T * a.H / 2;
+  combine_kernel<<<static_cast<int>(ceil_div(n2, kCombineBlock)), kCombineBlock, 0, st>>>(a.ybuf, a.ids, a.T, a.H,
                                                                                           a.k, a.E, a.out);
-  rc = check_launch("moe_combine");
+  const int rc = check_launch("moe_combine");
   if (rc) return rc;
   pm.mark(first + 3);
   return LQ_OK;
 }
 
-// plan -> G1 -> G2 -> combine (x_permuted: the router already wrote the
-// K-slot permuted x into the workspace; otherwise a permute kernel runs first)
-int moe_forward_impl(const void *x, bool x_permuted, int64_t T, int H, int I, int E, int k, const int8_t *q1,
-                     const float *s1, const int8_t *q2, const float *s2, int bits, int64_t group_w1,
-                     int64_t group_w2, int flags, const int32_t *topk_ids, const float *topk_weights, char *ws,
-                     void *out, hipStream_t st, ProfileMarks &pm, int first_mark) {
-  const WsLayout w = ws_layout(T, H, I, E, k);
-  const int64_t N = T * k;
-  const int64_t g1 = effective_group(H, group_w1);
-  const int64_t g2 = effective_group(I, group_w2);
-  // the folded form applies one scale per 128-wide K chunk
-  const bool folded = (flags & LQ_MOE_FOLDED_SCALES) && g1 % kKC == 0 && g2 % kKC == 0;
 
+// the plan's arguments over the workspace
+PlanArgs plan_args(const int32_t *topk_ids, int64_t T, int E, int k, char *ws, const WsLayout &w) {
   PlanArgs p;
   p.ids = topk_ids;
-  p.N = N;
+  p.N = T * k;
   p.E = E;
   p.counts = reinterpret_cast<int32_t *>(ws + w.counts);
   p.offsets = reinterpret_cast<int32_t *>(ws + w.offsets);
@@ -865,18 +1250,48 @@ int moe_forward_impl(const void *x, bool x_permuted, int64_t T, int H, int I, in
   p.srow = reinterpret_cast<int32_t *>(ws + w.srow);
   p.k = k;
   p.hdr = reinterpret_cast<PlanHeader *>(ws + w.hdr);
+  return p;
+}
+
+// does this layer run on the streaming GEMMs?
+bool uses_stream(int bits, int H, int I, int64_t group_w1, int64_t group_w2, int flags) {
+  return !(flags & LQ_MOE_GENERAL_KERNEL) &&
+         stream_eligible(bits, H, I, effective_group(H, group_w1), effective_group(I, group_w2));
+}
+
+// [x permute] -> [plan] -> G1 -> G2 -> combine.  The streaming GEMMs stage
+// x itself; the general ones need its K-slot permuted copy in the workspace
+// (x_permuted: already written by the router).  planned: the plan already
+// ran (the fused front kernel).
+int moe_forward_impl(const void *x, bool x_permuted, bool planned, int64_t T, int H, int I, int E, int k,
+                     const int8_t *q1, const float *s1, const int8_t *q2, const float *s2, int bits,
+                     int64_t group_w1, int64_t group_w2, int flags, const int32_t *topk_ids,
+                     const float *topk_weights, char *ws, void *out, hipStream_t st, ProfileMarks &pm,
+                     int first_mark) {
+  const WsLayout w = ws_layout(T, H, I, E, k);
+  const int64_t g1 = effective_group(H, group_w1);
+  const int64_t g2 = effective_group(I, group_w2);
+  // the folded form applies one scale per 128-wide K chunk
+  const bool folded = (flags & LQ_MOE_FOLDED_SCALES) && g1 % kKC == 0 && g2 % kKC == 0;
+  const bool stream = uses_stream(bits, H, I, group_w1, group_w2, flags);
+
+  const PlanArgs p = plan_args(topk_ids, T, E, k, ws, w);
   uint16_t *xperm = reinterpret_cast<uint16_t *>(ws + w.xperm);
-  if (!x_permuted) {
+  if (!stream && !x_permuted) {
     const int64_t n8 = T * H / 8;
     permute_rows_kernel<<<static_cast<int>(ceil_div(n8, 256)), 256, 0, st>>>(static_cast<const uint16_t *>(x), n8,
                                                                              xperm);
   }
-  plan_kernel<<<1, kPlanBlock, 0, st>>>(p);
-  int rc = check_launch("moe_plan");
-  if (rc) return rc;
+  int rc = LQ_OK;
+  if (!planned) {
+    plan_kernel<<<1, kPlanBlock, 0, st>>>(p);
+    rc = check_launch("moe_plan");
+    if (rc) return rc;
+  }
   pm.mark(first_mark);
 
   MoeArgs a;
+  a.x = static_cast<const uint16_t *>(x);
   a.xperm = xperm;
   a.q1 = q1;
   a.s1 = s1;
@@ -904,13 +1319,33 @@ int moe_forward_impl(const void *x, bool x_permuted, int64_t T, int H, int I, in
   const int64_t blocks = max_blocks_for(T, E, k);
   const int64_t max_g1 = blocks * (I / kF1), max_g2 = blocks * (H / kR2);
   if (bits == 4)
-    rc = folded ? launch_phases<4, true>(a, max_g1, max_g2, st, pm, first_mark)
-                : launch_phases<4, false>(a, max_g1, max_g2, st, pm, first_mark);
+    rc = folded ? launch_phases<4, true>(a, max_g1, max_g2, st, pm, first_mark, stream)
+                : launch_phases<4, false>(a, max_g1, max_g2, st, pm, first_mark, stream);
   else
-    rc = folded ? launch_phases<8, true>(a, max_g1, max_g2, st, pm, first_mark)
-                : launch_phases<8, false>(a, max_g1, max_g2, st, pm, first_mark);
+    rc = folded ? launch_phases<8, true>(a, max_g1, max_g2, st, pm, first_mark, stream)
+                : launch_phases<8, false>(a, max_g1, max_g2, st, pm, first_mark, stream);
   if (rc) return rc;
   return pm.rc;
+}
+
+// router + plan of a small layer as one launch (front_kernel)
+int launch_front(const void *logits, int logits_dtype, int64_t T, int E, int k, int renormalize, int32_t *ids,
+                 float *weights, char *ws, int H, int I, hipStream_t st) {
+  const WsLayout w = ws_layout(T, H, I, E, k);
+  const PlanArgs p = plan_args(ids, T, E, k, ws, w);
+#define LQ_FRONT_LAUNCH(EPL)                                                                                 \
+  LQ_DISPATCH_DTYPE(logits_dtype, LDT, {                                                                     \
+    front_kernel<LDT, EPL><<<1, kPlanBlock, 0, st>>>(p, logits, T, k, renormalize, weights);                 \
+  })
+  if (E <= 64) {
+    LQ_FRONT_LAUNCH(1);
+  } else if (E <= 128) {
+    LQ_FRONT_LAUNCH(2);
+  } else {
+    LQ_FRONT_LAUNCH(4);
+  }
+#undef LQ_FRONT_LAUNCH
+  return check_launch("moe_front");
 }
 
 ProfileMarks take_profile(hipStream_t st) {
@@ -965,8 +1400,8 @@ extern "C" int lq_moe_forward(const void *x, int64_t T, int H, int I, int E, int
   if (rc || T == 0) return rc;
   if (!topk_ids || !topk_weights) return fail(LQ_ERR_VALUE, "moe_forward: null routing pointer");
   pm.mark(0);
-  return moe_forward_impl(x, false, T, H, I, E, k, q1, s1, q2, s2, bits, group_w1, group_w2, flags, topk_ids,
-                          topk_weights, static_cast<char *>(workspace), out, st, pm, 1);
+  return moe_forward_impl(x, false, false, T, H, I, E, k, q1, s1, q2, s2, bits, group_w1, group_w2, flags,
+                          topk_ids, topk_weights, static_cast<char *>(workspace), out, st, pm, 1);
 }
 
 extern "C" int lq_moe_layer(const void *x, const void *logits, int logits_dtype, int64_t T, int H, int I, int E,
@@ -985,11 +1420,23 @@ extern "C" int lq_moe_layer(const void *x, const void *logits, int logits_dtype,
   int32_t *ids = topk_ids_out ? topk_ids_out : reinterpret_cast<int32_t *>(ws + w.ids);
   float *weights = reinterpret_cast<float *>(ws + w.weights);
   pm.mark(0);
-  // the router also writes the K-slot permuted copy of x the layer stages from
+  const bool streaming = uses_stream(bits, H, I, group_w1, group_w2, flags);
+  if (streaming && T * k <= kFrontMaxN) {
+    // router and plan in one launch (the route and plan marks coincide)
+    if (logits_dtype != LQ_F32 && logits_dtype != LQ_BF16 && logits_dtype != LQ_F16)
+      return fail(LQ_ERR_VALUE, "route_topk: logits must be float32, float16 or bfloat16");
+    rc = launch_front(logits, logits_dtype, T, E, k, renormalize, ids, weights, ws, H, I, st);
+    if (rc) return rc;
+    pm.mark(1);
+    return moe_forward_impl(x, true, true, T, H, I, E, k, q1, s1, q2, s2, bits, group_w1, group_w2, flags, ids,
+                            weights, ws, out, st, pm, 2);
+  }
+  // the general GEMMs stage the K-slot permuted copy of x the router writes
   rc = launch_route_topk(logits, logits_dtype, T, E, k, renormalize, ids, weights, st,
-                         static_cast<const uint16_t *>(x), H, reinterpret_cast<uint16_t *>(ws + w.xperm));
+                         static_cast<const uint16_t *>(x), H,
+                         streaming ? nullptr : reinterpret_cast<uint16_t *>(ws + w.xperm));
   if (rc) return rc;
   pm.mark(1);
-  return moe_forward_impl(x, true, T, H, I, E, k, q1, s1, q2, s2, bits, group_w1, group_w2, flags, ids, weights, ws,
-                          out, st, pm, 2);
+  return moe_forward_impl(x, true, false, T, H, I, E, k, q1, s1, q2, s2, bits, group_w1, group_w2, flags, ids,
+                          weights, ws, out, st, pm, 2);
 }

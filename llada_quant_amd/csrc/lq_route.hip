@@ -15,14 +15,9 @@ namespace {
 
 constexpr int kRouteBlock = 256;  // 4 tokens per block, one wave each
 
-// One wavefront per token; lane l holds experts l, l+64, ... (EPL of them).
-// Each expert's rank is counted directly: rank(e) = #{e' : x[e'] > x[e], or
-// x[e'] == x[e] and e' < e} over the token's logits (read back from LDS), so
-// ids come out in descending-logit order with ties to the lower expert id --
-// the order of descending probability, softmax being monotone -- with no
-// serial selection rounds.  Experts of rank < k write their id and fp32
-// softmax probability to slot `rank`.  With xperm != nullptr the wave also
-// copies its token's row of x into xperm in the MoE kernel's K-slot order.
+// One wavefront per token (route_token).  With xperm != nullptr the wave
+// also copies its token's row of x into xperm in the MoE kernel's K-slot
+// order.
 template <int LDT, int EPL>
 __global__ __launch_bounds__(kRouteBlock) void route_topk_kernel(const void *__restrict__ logits, int64_t T,
                                                                  int E, int k, int renorm,
@@ -30,59 +25,10 @@ __global__ __launch_bounds__(kRouteBlock) void route_topk_kernel(const void *__r
                                                                  float *__restrict__ weights,
                                                                  const uint16_t *__restrict__ x, int H,
                                                                  uint16_t *__restrict__ xperm) {
-  __shared__ float row[kRouteBlock / 64][kMaxExperts];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
   const int64_t t = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
   if (t >= T) return;  // uniform per wave; no block-wide barrier below
-  float v[EPL];
-  float m = -__builtin_inff();
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) {
-    const int e = lane + 64 * j;
-    v[j] = e < E ? load_f32<LDT>(logits, t * E + e) : -__builtin_inff();
-    if (e < E) row[wave][e] = v[j];
-    m = fmaxf(m, v[j]);
-  }
-  m = wave_max(m);
-  float p[EPL];
-  float s = 0.0f;
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) {
-    const int e = lane + 64 * j;
-    p[j] = e < E ? expf(v[j] - m) : 0.0f;
-    s += p[j];
-  }
-  s = wave_sum(s);
-  int rank[EPL];
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) rank[j] = 0;
-  // the wave's LDS row is written and read by this wave only (lockstep)
-  __builtin_amdgcn_wave_barrier();
-  for (int c = 0; c < E; ++c) {
-    const float xc = row[wave][c];
-#pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-      const int e = lane + 64 * j;
-      rank[j] += (xc > v[j] || (xc == v[j] && c < e)) ? 1 : 0;
-    }
-  }
-  float wsel = 0.0f;
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) {
-    const int e = lane + 64 * j;
-    if (e < E && rank[j] < k) wsel += p[j] / s;
-  }
-  const float wsum = renorm ? wave_sum(wsel) : 1.0f;
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) {
-    const int e = lane + 64 * j;
-    if (e < E && rank[j] < k) {
-      const float pw = p[j] / s;
-      ids[t * k + rank[j]] = e;
-      weights[t * k + rank[j]] = renorm ? pw / wsum : pw;
-    }
-  }
+  route_token<LDT, EPL>(logits, t, E, k, renorm, ids, weights, nullptr);
   if (xperm != nullptr) {
     const uint4 *src = reinterpret_cast<const uint4 *>(x + t * H);
     uint4 *dst = reinterpret_cast<uint4 *>(xperm + t * H);

@@ -192,3 +192,52 @@ def test_shape_mismatch_is_rejected_on_the_host(dev):
     w = torch.ones(4, 1, device=dev)
     with pytest.raises(ValueError, match="inconsistent shapes"):
         fused_moe_packed(x, q1, q2, ids, w)
+
+
+@pytest.mark.parametrize("bits,folded", [(4, False), (4, True), (8, False), (8, True)])
+@pytest.mark.parametrize("T,k,skew", [(48, 4, True), (300, 2, False), (7, 8, True)])
+def test_streaming_kernels_match_general_kernels(dev, bits, folded, T, k, skew):
+    """Shapes with K in whole 512-wide steps run the streaming GEMMs; the general
+    GEMMs do the same per-chunk arithmetic in the same order, so the two agree
+    bit for bit.  Cases: blocks of <= 16 and 17..32 rows, experts spanning
+    several row blocks, fewer units than compute units, empty experts."""
+    E, H, I = 16, 1024, 512
+    q1, q2 = make_layer(dev, E, H, I, bits, seed=T + bits)
+    g = torch.Generator().manual_seed(T)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    logits = zipf_logits(T, E, seed=T) if skew else torch.randn(T, E, generator=g)
+    ids, w = route_topk(logits.to(dev), k)
+    a = fused_moe_packed(x, q1, q2, ids, w, folded_scales=folded)
+    b = fused_moe_packed(x, q1, q2, ids, w, folded_scales=folded, general_kernel=True)
+    assert torch.equal(a, b)
+    assert_close(a, oracle_out(x, q1, q2, ids, w), bar(folded))
+
+
+def test_streaming_one_hot_expert_many_blocks(dev):
+    """One expert holds every token: 13 row blocks of one expert, all streamed."""
+    q1, q2 = make_layer(dev, 8, 512, 512, 4, seed=15)
+    T = 400
+    g = torch.Generator().manual_seed(15)
+    x = torch.randn(T, 512, generator=g).to(torch.bfloat16).to(dev)
+    ids = torch.full((T, 1), 3, dtype=torch.int32, device=dev)
+    w = torch.rand(T, 1, generator=g).to(dev)
+    out = fused_moe_packed(x, q1, q2, ids, w)
+    assert torch.equal(out, fused_moe_packed(x, q1, q2, ids, w, general_kernel=True))
+    assert_close(out, oracle_out(x, q1, q2, ids, w))
+
+
+@pytest.mark.parametrize("T,k", [(64, 8), (600, 8)])
+def test_moe_layer_front_end_matches_router_then_forward(dev, T, k):
+    """moe_layer on a streaming shape: T*k <= 2048 takes the one-launch router + plan,
+    larger T the router kernel then the plan; both equal route_topk + fused_moe_packed."""
+    E, H, I = 32, 1024, 512
+    q1, q2 = make_layer(dev, E, H, I, 4, seed=T)
+    g = torch.Generator().manual_seed(T + 1)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    logits = zipf_logits(T, E, seed=T).to(dev)
+    out, ids = moe_layer(x, logits, q1, q2, top_k=k)
+    ids2, w2 = route_topk(logits, k)
+    assert torch.equal(ids, ids2)
+    ref = fused_moe_packed(x, q1, q2, ids2, w2)
+    assert torch.equal(out, ref)
+    assert_close(out, oracle_out(x, q1, q2, ids2, w2))
