@@ -95,13 +95,21 @@ class Hip:
     def __init__(self):
         self.lib = ctypes.CDLL("libamdhip64.so.7")
         self.lib.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.lib.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
         self.lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
         self.lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
         self.lib.hipEventSynchronize.argtypes = [ctypes.c_void_p]
 
-    def event(self):
+    # timing-only events: no system-scope fence (no L2 writeback / invalidate
+    # when recorded), so a marker between two kernels costs next to nothing
+    DISABLE_SYSTEM_FENCE = 0x20000000
+
+    def event(self, light=False):
         ev = ctypes.c_void_p()
-        rc = self.lib.hipEventCreate(ctypes.byref(ev))
+        if light:
+            rc = self.lib.hipEventCreateWithFlags(ctypes.byref(ev), self.DISABLE_SYSTEM_FENCE)
+        else:
+            rc = self.lib.hipEventCreate(ctypes.byref(ev))
         if rc != 0:
             raise RuntimeError(f"hipEventCreate failed ({rc})")
         return ev
@@ -285,42 +293,54 @@ def main():
     n_marks = 6
 
     def timed(calls, steps, warmup):
-        """(ms per step, mean ms per stage [route, plan, gemm1, gemm2, combine]) over `steps` steps."""
+        """ms per step of `steps` layer calls, no markers inside the timed region."""
         for i in range(warmup):
             rc = lib.lq_moe_layer(*calls[i % len(calls)])
             if rc:
                 _lib.check(rc, "moe_layer")
-        torch.cuda.synchronize()
-        marks = [[hip.event() for _ in range(n_marks)] for _ in range(steps)]
-        arrays = [(ctypes.c_void_p * n_marks)(*[m.value for m in row]) for row in marks]
         t_start, t_end = hip.event(), hip.event()
         torch.cuda.synchronize()  # barrier (one rank) + sync on both sides of the timed region
         hip.lib.hipEventRecord(t_start, hip_stream)
         for i in range(steps):
-            lib.lq_moe_profile_events(ctypes.cast(arrays[i], ctypes.c_void_p), n_marks)
             rc = lib.lq_moe_layer(*calls[i % len(calls)])
             if rc:
                 _lib.check(rc, "moe_layer")
         hip.lib.hipEventRecord(t_end, hip_stream)
         torch.cuda.synchronize()
         total_ms = hip.elapsed_ms(t_start, t_end)
+        hip.destroy(t_start)
+        hip.destroy(t_end)
+        return total_ms / steps
+
+    def staged(calls, steps):
+        """Mean ms per stage [route, plan, gemm1, gemm2, combine] over `steps` layer calls, from
+        fence-free HIP events the library records on its stream at the kernel boundaries."""
+        marks = [[hip.event(light=True) for _ in range(n_marks)] for _ in range(steps)]
+        arrays = [(ctypes.c_void_p * n_marks)(*[m.value for m in row]) for row in marks]
+        torch.cuda.synchronize()
+        for i in range(steps):
+            lib.lq_moe_profile_events(ctypes.cast(arrays[i], ctypes.c_void_p), n_marks)
+            rc = lib.lq_moe_layer(*calls[i % len(calls)])
+            if rc:
+                _lib.check(rc, "moe_layer")
+        torch.cuda.synchronize()
         stage_ms = [sum(hip.elapsed_ms(row[j], row[j + 1]) for row in marks) / steps for j in range(n_marks - 1)]
         for row in marks:
             for m in row:
                 hip.destroy(m)
-        hip.destroy(t_start)
-        hip.destroy(t_end)
-        return total_ms / steps, stage_ms
+        return stage_ms
 
     calls = make_calls(_lib.LQ_MOE_FOLDED_SCALES if args.folded else 0)
     wall0 = time.perf_counter()
-    ms_per_step, stage_ms = timed(calls, args.steps, args.warmup)
+    ms_per_step = timed(calls, args.steps, args.warmup)
     wall = time.perf_counter() - wall0
+    stage_ms = staged(calls, args.steps)
     value = T / (ms_per_step / 1e3)
     n_active = int((torch.bincount(ids.reshape(-1).long(), minlength=E) > 0).sum())
     layer_b, g1_b, g2_b = layer_bytes(cfg, n_active)
     gemm1_ms = stage_ms[2]
-    kname = "moe_gemm_kernel<G1> (W1 gate+up, SwiGLU epilogue; persistent)"
+    kname = ("moe_stream_kernel<G1> (W1 gate and up tiles streamed per CU, in-kernel block plan)"
+             if H % 512 == 0 and I % 512 == 0 else "moe_gemm_kernel<G1> (W1 gate+up, SwiGLU epilogue; persistent)")
     if cfg["bound"] == "hbm":
         achieved = g1_b / (gemm1_ms / 1e3) / 1e9
         roofline = {"kernel": kname, "bound": "hbm", "achieved": round(achieved, 1), "peak": MI355X_HBM_GBPS,
@@ -334,8 +354,9 @@ def main():
                     "algorithmic_flops": flops, "avg_ms": round(gemm1_ms, 5)}
     stages = {name: round(v, 5) for name, v in zip(("route", "plan", "gemm1", "gemm2", "combine"), stage_ms)}
     stages["gemm2_gbps"] = round(g2_b / (stage_ms[3] / 1e3) / 1e9, 1)
-    other_ms, other_stage = timed(make_calls(0 if args.folded else _lib.LQ_MOE_FOLDED_SCALES),
-                                  max(10, args.steps // 4), 3)
+    other_calls = make_calls(0 if args.folded else _lib.LQ_MOE_FOLDED_SCALES)
+    other_ms = timed(other_calls, max(10, args.steps // 4), 3)
+    other_stage = staged(other_calls, max(10, args.steps // 4))
 
     result = {
         "metric": "MoE-layer tokens/s W4A16 64E top-8 H2048; % HBM/MFMA roofline",

@@ -541,6 +541,34 @@ __global__ __launch_bounds__(kThreads, 3) void moe_gemm_kernel(MoeArgs a) {
   }
 }
 
+// exclusive scan of in[0..E) by wave 0 (lane l owns entries 4l..4l+3)
+__device__ void wave0_exclusive_scan(const int *in, int *out, int E, int *total) {
+  const int lane = threadIdx.x & 63;
+  int v[4];
+  int local = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = 4 * lane + i;
+    v[i] = e < E ? in[e] : 0;
+    local += v[i];
+  }
+  int incl = local;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  int run = incl - local;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = 4 * lane + i;
+    if (e < E) out[e] = run;
+    run += v[i];
+  }
+  const int tot = __shfl(incl, 63, 64);
+  if (lane == 0) *total = tot;
+}
+
 // ---------------------------------------------------------------------------
 // streaming G1 / G2 kernels (the weight-bandwidth regime)
 //
@@ -569,6 +597,8 @@ constexpr int kSThreads = 64 * kSWaves;
 // LDS bytes of the streaming kernels for reduction length K (token rows of
 // one block for the whole K)
 inline size_t stream_lds_bytes(int K) { return static_cast<size_t>(K) * kRowsMax * 2; }
+// upper bound of the static LDS of the streaming kernels (block_plan's tables)
+constexpr size_t kStaticLds = 8192;
 
 // reference op order (INFERENCE_REPO_CHANGES.md:296-309): g, u -> bf16;
 // silu in fp32 -> bf16; bf16 product
@@ -583,7 +613,8 @@ __device__ __forceinline__ uint16_t swiglu_bf16(float g, float u) {
 // G1 copies x into K-slot order; G2 builds act = SwiGLU(g, u) from
 // the gate / up pre-activations and permutes it into K-slot order.
 template <bool FIRST>
-__device__ __forceinline__ void stage_block(const MoeArgs &a, int row0, int rows, unsigned char *lds) {
+__device__ __forceinline__ void stage_block(const MoeArgs &a, int row0, int rows, const int32_t *rtok,
+                                            unsigned char *lds) {
   const int K = FIRST ? a.H : a.I;
   const int nk = K / kKC;
   const int per_row = nk * 16;  // 16-byte pieces (8 values) per row
@@ -603,7 +634,7 @@ __device__ __forceinline__ void stage_block(const MoeArgs &a, int row0, int rows
       const int rem = q - r * per_row;
       const int c = rem >> 4, pc = rem & 15;
       if constexpr (FIRST) {
-        const int64_t src = static_cast<int64_t>(a.srow[row0 + r]) * a.H + c * kKC + pc * 8;
+        const int64_t src = static_cast<int64_t>(rtok[r]) * a.H + c * kKC + pc * 8;
         v[i] = *reinterpret_cast<const u32x4 *>(a.x + src);
       } else {
         const int64_t src = static_cast<int64_t>(row0 + r) * (2 * a.I) + c * kKC + pc * 8;
@@ -636,8 +667,8 @@ __device__ __forceinline__ void stage_block(const MoeArgs &a, int row0, int rows
 }
 
 template <int BITS, bool FOLDED, bool FIRST, int NRT, int KD, bool SQ>
-__device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, int rows, int u_first, int u_end,
-                                             const unsigned char *lds) {
+__device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, int rows, const int32_t *rtok,
+                                             const int32_t *rasg, int u_first, int u_end, unsigned char *lds) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int lc = lane & 15;
@@ -726,7 +757,7 @@ __device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, 
             // gate (u < I / 16) or up pre-activation, rounded to bf16
             a.act[static_cast<int64_t>(row0 + m) * (2 * a.I) + 16 * u + lc] = f32_to_bf16_bits(tot[rt][0][j]);
           } else {
-            const int asg = a.sorted[row0 + m];
+            const int asg = rasg[m];
             a.ybuf[static_cast<int64_t>(asg) * a.H + 16 * u + lc] = tot[rt][0][j] * a.topk_w[asg];
           }
         }
@@ -750,7 +781,7 @@ __device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, 
   }
   // the block's token rows are staged while the first codes are in flight
   __syncthreads();  // the previous block's rows are no longer read
-  stage_block<FIRST>(a, row0, rows, const_cast<unsigned char *>(lds));
+  stage_block<FIRST>(a, row0, rows, rtok, lds);
   __syncthreads();
   if (nsteps == 0) return;
   int cu = f0, cc = 0;  // compute cursor: unit, first chunk of the current KD steps
@@ -802,37 +833,129 @@ __device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, 
 }
 
 template <int BITS, bool FOLDED, bool FIRST, int KD, bool SQ>
-__device__ __forceinline__ void stream_block(const MoeArgs &a, int blk, int u_first, int u_end,
-                                             unsigned char *lds) {
-  const int4 bi = a.blocks[blk];
-  const int e = __builtin_amdgcn_readfirstlane(bi.x);
-  const int row0 = __builtin_amdgcn_readfirstlane(bi.y);
-  const int rows = __builtin_amdgcn_readfirstlane(bi.z);
+__device__ __forceinline__ void stream_block(const MoeArgs &a, int e, int row0, int rows, const int32_t *rtok,
+                                             const int32_t *rasg, int u_first, int u_end, unsigned char *lds) {
   if (rows <= 16)
-    stream_units<BITS, FOLDED, FIRST, 1, KD, SQ>(a, e, row0, rows, u_first, u_end, lds);
+    stream_units<BITS, FOLDED, FIRST, 1, KD, SQ>(a, e, row0, rows, rtok, rasg, u_first, u_end, lds);
   else
-    stream_units<BITS, FOLDED, FIRST, 2, KD, SQ>(a, e, row0, rows, u_first, u_end, lds);
+    stream_units<BITS, FOLDED, FIRST, 2, KD, SQ>(a, e, row0, rows, rtok, rasg, u_first, u_end, lds);
 }
 
-template <int BITS, bool FOLDED, bool FIRST, int KD, bool SQ>
+// CU c of G and its share of nb blocks: with nb <= G, CUs
+// [ceil(b G / nb), ceil((b+1) G / nb)) share block b, CU c taking units
+// [i upb / m, (i+1) upb / m) of it; returns false for a CU without a block
+__device__ __forceinline__ bool cu_share(int c, int G, int nb, int upb, int &b, int &ub, int &ue) {
+  b = static_cast<int>(static_cast<int64_t>(c) * nb / G);
+  if (b >= nb) return false;
+  const int first = static_cast<int>((static_cast<int64_t>(b) * G + nb - 1) / nb);
+  const int next = static_cast<int>((static_cast<int64_t>(b + 1) * G + nb - 1) / nb);
+  const int m = next - first, i = c - first;
+  ub = i * upb / m;
+  ue = (i + 1) * upb / m;
+  return true;
+}
+
+// Small layers (T*k <= kPlanMaxN): every workgroup derives the plan of its
+// own block from the T*k routed ids instead of reading plan_kernel's
+// output -- the same per-expert counts and offsets, the same expert-major
+// blocks of <= 32 rows, and the block's assignments in ascending flat index
+// (plan_kernel's stable order), so the sorted row numbers G1 writes and G2
+// reads agree.  Fills rtok / rasg (token and assignment of each row) and
+// returns false when the CU has no block.
+constexpr int kPlanMaxN = 2048;
+__device__ __forceinline__ bool block_plan(const MoeArgs &a, int upb, int &e, int &row0, int &rows, int &ub,
+                                           int &ue, int32_t *rtok, int32_t *rasg) {
+  __shared__ int cnt[kMaxExperts];
+  __shared__ int off[kMaxExperts];
+  __shared__ int nbk[kMaxExperts];
+  __shared__ int nbs[kMaxExperts + 1];
+  __shared__ int wcount[kSWaves];
+  __shared__ int total;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int N = static_cast<int>(a.T * a.k);
+  const int E = a.E;
+  for (int i = tid; i < E; i += kSThreads) cnt[i] = 0;
+  __syncthreads();
+  for (int i = tid; i < N; i += kSThreads) {
+    const int id = a.ids[i];
+    if (id >= 0 && id < E) atomicAdd(&cnt[id], 1);
+  }
+  __syncthreads();
+  if (wave == 0) {
+    wave0_exclusive_scan(cnt, off, E, &total);
+  } else if (wave == 1) {
+    // blocks per expert and their scan (wave 1 writes nbk, then scans it)
+    for (int i = lane; i < E; i += 64) nbk[i] = (cnt[i] + kRowsMax - 1) / kRowsMax;
+    __builtin_amdgcn_wave_barrier();
+    wave0_exclusive_scan(nbk, nbs, E, &nbs[E]);
+  }
+  __syncthreads();
+  const int nb = nbs[E];
+  int b;
+  if (!cu_share(blockIdx.x, gridDim.x, nb, upb, b, ub, ue)) return false;
+  int lo = 0, hi = E;  // largest expert with nbs[expert] <= b
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (nbs[mid] <= b) lo = mid;
+    else hi = mid;
+  }
+  e = __builtin_amdgcn_readfirstlane(lo);
+  const int first = (b - nbs[e]) * kRowsMax;  // rank of the block's first row within expert e
+  rows = __builtin_amdgcn_readfirstlane(min(kRowsMax, cnt[e] - first));
+  row0 = __builtin_amdgcn_readfirstlane(off[e] + first);
+  // stable compaction of expert e's assignments, keeping ranks [first, first + rows)
+  const unsigned long long lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  int run = 0;
+  for (int c0 = 0; c0 < N; c0 += kSThreads) {
+    const int i = c0 + tid;
+    const bool hit = i < N && a.ids[i] == e;
+    const unsigned long long bal = __ballot(hit);
+    if (lane == 0) wcount[wave] = __popcll(bal);
+    __syncthreads();
+    int before = run;
+    for (int w = 0; w < wave; ++w) before += wcount[w];
+    const int rank = before + __popcll(bal & lt);
+    if (hit && rank >= first && rank < first + rows) {
+      rasg[rank - first] = i;
+      rtok[rank - first] = i / a.k;
+    }
+    for (int w = 0; w < kSWaves; ++w) run += wcount[w];
+    __syncthreads();
+  }
+  __syncthreads();
+  return true;
+}
+
+template <int BITS, bool FOLDED, bool FIRST, int KD, bool SQ, bool INPLAN>
 __global__ __launch_bounds__(kSThreads, 1) void moe_stream_kernel(MoeArgs a) {
   extern __shared__ __align__(16) unsigned char slds[];
   const int upb = FIRST ? 2 * a.I / 16 : a.H / 16;  // units (16-row tiles) per row block
-  const int nb = __builtin_amdgcn_readfirstlane(a.hdr->n_blk);
-  const int G = gridDim.x, c = blockIdx.x;
-  if (nb <= G) {
-    // CUs [ceil(b G / nb), ceil((b+1) G / nb)) share block b
-    const int b = static_cast<int>(static_cast<int64_t>(c) * nb / G);
-    if (b >= nb) return;
-    const int first = static_cast<int>((static_cast<int64_t>(b) * G + nb - 1) / nb);
-    const int next = static_cast<int>((static_cast<int64_t>(b + 1) * G + nb - 1) / nb);
-    const int m = next - first, i = c - first;
-    const int ub = i * upb / m, ue = (i + 1) * upb / m;
-    stream_block<BITS, FOLDED, FIRST, KD, SQ>(a, b, ub, ue, slds);
+  if constexpr (INPLAN) {
+    __shared__ int32_t rtok[kRowsMax], rasg[kRowsMax];
+    int e, row0, rows, ub, ue;
+    if (!block_plan(a, upb, e, row0, rows, ub, ue, rtok, rasg)) return;
+    stream_block<BITS, FOLDED, FIRST, KD, SQ>(a, e, row0, rows, rtok, rasg, ub, ue, slds);
   } else {
-    const int b0 = static_cast<int>(static_cast<int64_t>(c) * nb / G);
-    const int b1 = static_cast<int>(static_cast<int64_t>(c + 1) * nb / G);
-    for (int b = b0; b < b1; ++b) stream_block<BITS, FOLDED, FIRST, KD, SQ>(a, b, 0, upb, slds);
+    const int nb = __builtin_amdgcn_readfirstlane(a.hdr->n_blk);
+    const int G = gridDim.x, c = blockIdx.x;
+    auto run_block = [&](int b, int ub, int ue) __attribute__((always_inline)) {
+      const int4 bi = a.blocks[b];
+      const int e = __builtin_amdgcn_readfirstlane(bi.x);
+      const int row0 = __builtin_amdgcn_readfirstlane(bi.y);
+      const int rows = __builtin_amdgcn_readfirstlane(bi.z);
+      stream_block<BITS, FOLDED, FIRST, KD, SQ>(a, e, row0, rows, a.srow + row0, a.sorted + row0, ub, ue, slds);
+    };
+    if (nb <= G) {
+      int b, ub, ue;
+      if (!cu_share(c, G, nb, upb, b, ub, ue)) return;
+      run_block(b, ub, ue);
+    } else {
+      const int b0 = static_cast<int>(static_cast<int64_t>(c) * nb / G);
+      const int b1 = static_cast<int>(static_cast<int64_t>(c + 1) * nb / G);
+      for (int b = b0; b < b1; ++b) run_block(b, 0, upb);
+    }
   }
 }
 
@@ -856,34 +979,6 @@ struct PlanArgs {
   int4 *blocks;
   PlanHeader *hdr;
 };
-
-// exclusive scan of in[0..E) by wave 0 (lane l owns entries 4l..4l+3)
-__device__ void wave0_exclusive_scan(const int *in, int *out, int E, int *total) {
-  const int lane = threadIdx.x & 63;
-  int v[4];
-  int local = 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = 4 * lane + i;
-    v[i] = e < E ? in[e] : 0;
-    local += v[i];
-  }
-  int incl = local;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(incl, o, 64);
-    if (lane >= o) incl += y;
-  }
-  int run = incl - local;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = 4 * lane + i;
-    if (e < E) out[e] = run;
-    run += v[i];
-  }
-  const int tot = __shfl(incl, 63, 64);
-  if (lane == 0) *total = tot;
-}
 
 // the plan for one workgroup of kPlanBlock threads; id_at(a) returns the
 // expert of assignment a (read from memory or from LDS)
@@ -981,21 +1076,6 @@ __device__ __forceinline__ void plan_body(const PlanArgs &p, IdAt id_at) {
 
 __global__ __launch_bounds__(kPlanBlock) void plan_kernel(PlanArgs p) {
   plan_body(p, [&](int64_t a) { return p.ids[a]; });
-}
-
-// Front end of a small layer in one workgroup: the router (one wave per
-// token, route_token) writes ids and weights and keeps the ids in LDS, then
-// the plan runs on them -- one launch instead of two.
-constexpr int kFrontMaxN = 2048;  // assignments T * k the front kernel takes
-template <int LDT, int EPL>
-__global__ __launch_bounds__(kPlanBlock) void front_kernel(PlanArgs p, const void *logits, int64_t T, int k,
-                                                          int renorm, float *weights) {
-  __shared__ int32_t ids_lds[kFrontMaxN];
-  const int wave = threadIdx.x >> 6;
-  for (int64_t t = wave; t < T; t += kPlanWaves)
-    route_token<LDT, EPL>(logits, t, p.E, k, renorm, const_cast<int32_t *>(p.ids), weights, ids_lds);
-  __syncthreads();
-  plan_body(p, [&](int64_t a) { return ids_lds[a]; });
 }
 
 // x [rows, H] -> xperm, each group of 8 bf16 in K-slot order (8 values per thread)
@@ -1155,42 +1235,58 @@ DeviceInfo device_info() {
 bool stream_eligible(int bits, int H, int I, int64_t g1, int64_t g2) {
   const int step = kKC * (bits == 4 ? 4 : 2);
   const size_t lds = stream_lds_bytes(std::max(H, I));
+  // (kStaticLds: what the streaming kernels declare statically)
   return H % step == 0 && I % step == 0 && g1 % kKC == 0 && g2 % kKC == 0 &&
-         lds <= static_cast<size_t>(device_info().max_lds);
+         lds + kStaticLds <= static_cast<size_t>(device_info().max_lds);
 }
 
-template <int BITS, bool FOLDED, bool FIRST, int KD, bool SQ>
+template <int BITS, bool FOLDED, bool FIRST, int KD, bool SQ, bool INPLAN>
 int launch_stream_kd(const MoeArgs &a, hipStream_t st) {
   const DeviceInfo dev = device_info();
   static std::once_flag attr_once;
   static hipError_t attr_rc = hipSuccess;
   std::call_once(attr_once, [&] {
-    attr_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(moe_stream_kernel<BITS, FOLDED, FIRST, KD, SQ>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, dev.max_lds);
+    // dynamic LDS may take what the kernel's static LDS leaves
+    const void *fn = reinterpret_cast<const void *>(moe_stream_kernel<BITS, FOLDED, FIRST, KD, SQ, INPLAN>);
+    hipFuncAttributes fa{};
+    attr_rc = hipFuncGetAttributes(&fa, fn);
+    if (attr_rc == hipSuccess)
+      attr_rc = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    dev.max_lds - static_cast<int>(fa.sharedSizeBytes));
   });
   if (attr_rc != hipSuccess)
     return fail(LQ_ERR_RUNTIME, std::string("hipFuncSetAttribute failed: ") + hipGetErrorString(attr_rc));
   const size_t lds = stream_lds_bytes(FIRST ? a.H : a.I);
-  moe_stream_kernel<BITS, FOLDED, FIRST, KD, SQ><<<dev.cus, kSThreads, lds, st>>>(a);
+  moe_stream_kernel<BITS, FOLDED, FIRST, KD, SQ, INPLAN><<<dev.cus, kSThreads, lds, st>>>(a);
   return check_launch(FIRST ? "moe_stream_gemm1" : "moe_stream_gemm2");
 }
 
 // chunks in flight per wave: 8 KB of codes where K allows (INT4: 8 x 1 KB,
 // INT8: 4 x 2 KB), half that otherwise; the folded INT4 form keeps 4 (its
 // extra accumulators leave no registers for 8)
+template <int BITS, bool FOLDED, bool FIRST, int KD, bool SQ>
+int launch_stream_plan(const MoeArgs &a, hipStream_t st, bool inplan) {
+  return inplan ? launch_stream_kd<BITS, FOLDED, FIRST, KD, SQ, true>(a, st)
+                : launch_stream_kd<BITS, FOLDED, FIRST, KD, SQ, false>(a, st);
+}
+
+// chunks in flight per wave: 8 KB of codes where K allows (INT4: 8 x 1 KB,
+// INT8: 4 x 2 KB), half that otherwise; the folded INT4 form keeps 4 (its
+// extra accumulators leave no registers for 8).  inplan: the kernels plan
+// their blocks themselves (small layers; no plan_kernel ran).
 template <int BITS, bool FOLDED, bool FIRST>
-int launch_stream(const MoeArgs &a, hipStream_t st) {
+int launch_stream(const MoeArgs &a, hipStream_t st, bool inplan) {
   const int nk = (FIRST ? a.H : a.I) / kKC;
   constexpr int kDeep = BITS == 4 ? (FOLDED ? 4 : 8) : 4;
   // per-unit scale loads: group length 128, at most 16 groups, runs of 4
   const bool sq = (FIRST ? a.g1 : a.g2) == kKC && nk <= 16;
   if (nk % kDeep == 0)
-    return sq ? launch_stream_kd<BITS, FOLDED, FIRST, kDeep, true>(a, st)
-              : launch_stream_kd<BITS, FOLDED, FIRST, kDeep, false>(a, st);
+    return sq ? launch_stream_plan<BITS, FOLDED, FIRST, kDeep, true>(a, st, inplan)
+              : launch_stream_plan<BITS, FOLDED, FIRST, kDeep, false>(a, st, inplan);
   if constexpr (kDeep / 2 >= 4) {
-    if (sq) return launch_stream_kd<BITS, FOLDED, FIRST, kDeep / 2, true>(a, st);
+    if (sq) return launch_stream_plan<BITS, FOLDED, FIRST, kDeep / 2, true>(a, st, inplan);
   }
-  return launch_stream_kd<BITS, FOLDED, FIRST, kDeep / 2, false>(a, st);
+  return launch_stream_plan<BITS, FOLDED, FIRST, kDeep / 2, false>(a, st, inplan);
 }
 
 template <int BITS, bool FOLDED>
@@ -1215,12 +1311,12 @@ int launch_general(const MoeArgs &a, int64_t max_g1, int64_t max_g2, hipStream_t
 
 template <int BITS, bool FOLDED>
 int launch_phases(const MoeArgs &a, int64_t max_g1, int64_t max_g2, hipStream_t st, ProfileMarks &pm, int first,
-                  bool stream) {
+                  bool stream, bool inplan) {
   if (stream) {
-    int rc = launch_stream<BITS, FOLDED, true>(a, st);
+    int rc = launch_stream<BITS, FOLDED, true>(a, st, inplan);
     if (rc) return rc;
     pm.mark(first + 1);
-    rc = launch_stream<BITS, FOLDED, false>(a, st);
+    rc = launch_stream<BITS, FOLDED, false>(a, st, inplan);
     if (rc) return rc;
     pm.mark(first + 2);
   } else {
@@ -1261,9 +1357,8 @@ bool uses_stream(int bits, int H, int I, int64_t group_w1, int64_t group_w2, int
 
 // [x permute] -> [plan] -> G1 -> G2 -> combine.  The streaming GEMMs stage
 // x itself; the general ones need its K-slot permuted copy in the workspace
-// (x_permuted: already written by the router).  planned: the plan already
-// ran (the fused front kernel).
-int moe_forward_impl(const void *x, bool x_permuted, bool planned, int64_t T, int H, int I, int E, int k,
+// (x_permuted: already written by the router).
+int moe_forward_impl(const void *x, bool x_permuted, int64_t T, int H, int I, int E, int k,
                      const int8_t *q1, const float *s1, const int8_t *q2, const float *s2, int bits,
                      int64_t group_w1, int64_t group_w2, int flags, const int32_t *topk_ids,
                      const float *topk_weights, char *ws, void *out, hipStream_t st, ProfileMarks &pm,
@@ -1282,8 +1377,10 @@ int moe_forward_impl(const void *x, bool x_permuted, bool planned, int64_t T, in
     permute_rows_kernel<<<static_cast<int>(ceil_div(n8, 256)), 256, 0, st>>>(static_cast<const uint16_t *>(x), n8,
                                                                              xperm);
   }
+  // small layers on the streaming GEMMs plan their blocks in-kernel
+  const bool inplan = stream && T * k <= kPlanMaxN;
   int rc = LQ_OK;
-  if (!planned) {
+  if (!inplan) {
     plan_kernel<<<1, kPlanBlock, 0, st>>>(p);
     rc = check_launch("moe_plan");
     if (rc) return rc;
@@ -1319,33 +1416,13 @@ int moe_forward_impl(const void *x, bool x_permuted, bool planned, int64_t T, in
   const int64_t blocks = max_blocks_for(T, E, k);
   const int64_t max_g1 = blocks * (I / kF1), max_g2 = blocks * (H / kR2);
   if (bits == 4)
-    rc = folded ? launch_phases<4, true>(a, max_g1, max_g2, st, pm, first_mark, stream)
-                : launch_phases<4, false>(a, max_g1, max_g2, st, pm, first_mark, stream);
+    rc = folded ? launch_phases<4, true>(a, max_g1, max_g2, st, pm, first_mark, stream, inplan)
+                : launch_phases<4, false>(a, max_g1, max_g2, st, pm, first_mark, stream, inplan);
   else
-    rc = folded ? launch_phases<8, true>(a, max_g1, max_g2, st, pm, first_mark, stream)
-                : launch_phases<8, false>(a, max_g1, max_g2, st, pm, first_mark, stream);
+    rc = folded ? launch_phases<8, true>(a, max_g1, max_g2, st, pm, first_mark, stream, inplan)
+                : launch_phases<8, false>(a, max_g1, max_g2, st, pm, first_mark, stream, inplan);
   if (rc) return rc;
   return pm.rc;
-}
-
-// router + plan of a small layer as one launch (front_kernel)
-int launch_front(const void *logits, int logits_dtype, int64_t T, int E, int k, int renormalize, int32_t *ids,
-                 float *weights, char *ws, int H, int I, hipStream_t st) {
-  const WsLayout w = ws_layout(T, H, I, E, k);
-  const PlanArgs p = plan_args(ids, T, E, k, ws, w);
-#define LQ_FRONT_LAUNCH(EPL)                                                                                 \
-  LQ_DISPATCH_DTYPE(logits_dtype, LDT, {                                                                     \
-    front_kernel<LDT, EPL><<<1, kPlanBlock, 0, st>>>(p, logits, T, k, renormalize, weights);                 \
-  })
-  if (E <= 64) {
-    LQ_FRONT_LAUNCH(1);
-  } else if (E <= 128) {
-    LQ_FRONT_LAUNCH(2);
-  } else {
-    LQ_FRONT_LAUNCH(4);
-  }
-#undef LQ_FRONT_LAUNCH
-  return check_launch("moe_front");
 }
 
 ProfileMarks take_profile(hipStream_t st) {
@@ -1400,7 +1477,7 @@ extern "C" int lq_moe_forward(const void *x, int64_t T, int H, int I, int E, int
   if (rc || T == 0) return rc;
   if (!topk_ids || !topk_weights) return fail(LQ_ERR_VALUE, "moe_forward: null routing pointer");
   pm.mark(0);
-  return moe_forward_impl(x, false, false, T, H, I, E, k, q1, s1, q2, s2, bits, group_w1, group_w2, flags,
+  return moe_forward_impl(x, false, T, H, I, E, k, q1, s1, q2, s2, bits, group_w1, group_w2, flags,
                           topk_ids, topk_weights, static_cast<char *>(workspace), out, st, pm, 1);
 }
 
@@ -1421,22 +1498,12 @@ extern "C" int lq_moe_layer(const void *x, const void *logits, int logits_dtype,
   float *weights = reinterpret_cast<float *>(ws + w.weights);
   pm.mark(0);
   const bool streaming = uses_stream(bits, H, I, group_w1, group_w2, flags);
-  if (streaming && T * k <= kFrontMaxN) {
-    // router and plan in one launch (the route and plan marks coincide)
-    if (logits_dtype != LQ_F32 && logits_dtype != LQ_BF16 && logits_dtype != LQ_F16)
-      return fail(LQ_ERR_VALUE, "route_topk: logits must be float32, float16 or bfloat16");
-    rc = launch_front(logits, logits_dtype, T, E, k, renormalize, ids, weights, ws, H, I, st);
-    if (rc) return rc;
-    pm.mark(1);
-    return moe_forward_impl(x, true, true, T, H, I, E, k, q1, s1, q2, s2, bits, group_w1, group_w2, flags, ids,
-                            weights, ws, out, st, pm, 2);
-  }
   // the general GEMMs stage the K-slot permuted copy of x the router writes
   rc = launch_route_topk(logits, logits_dtype, T, E, k, renormalize, ids, weights, st,
                          static_cast<const uint16_t *>(x), H,
                          streaming ? nullptr : reinterpret_cast<uint16_t *>(ws + w.xperm));
   if (rc) return rc;
   pm.mark(1);
-  return moe_forward_impl(x, true, false, T, H, I, E, k, q1, s1, q2, s2, bits, group_w1, group_w2, flags, ids,
+  return moe_forward_impl(x, true, T, H, I, E, k, q1, s1, q2, s2, bits, group_w1, group_w2, flags, ids,
                           weights, ws, out, st, pm, 2);
 }
