@@ -185,8 +185,10 @@ size_t lq_moe_workspace_bytes(int64_t T, int H, int I, int E, int k);
  *           contribute nothing
  *   workspace of ws_bytes >= lq_moe_workspace_bytes(T, H, I, E, k)
  * Requires H % 128 == 0, I % 64 == 0, group lengths (after the per-row
- * fallback) that are multiples of 32, and T <= 262144.  Kernels on `stream`
- * (x permute, plan, GEMM1, GEMM2, combine); no host synchronisation.
+ * fallback) that are multiples of 32, and T <= 262144.  Kernels on `stream`:
+ * the expert plan (skipped when T*k <= 2048 and the streaming GEMMs derive it
+ * themselves), GEMM1, GEMM2, combine; the general GEMMs add an x permute in
+ * front.  No host synchronisation.
  */
 int lq_moe_forward(const void *x, int64_t T, int H, int I, int E, int k,
                    const int8_t *q1, const float *s1, const int8_t *q2,
@@ -217,8 +219,11 @@ int lq_moe_layer(const void *x, const void *logits, int logits_dtype,
  * hipEvent_t handles that the NEXT lq_moe_forward / lq_moe_layer call on
  * this thread records on its stream: events[0] before its first kernel and
  * events[i] after the i-th stage (layer: route, plan, GEMM1, GEMM2, combine;
- * forward: x permute + plan, GEMM1, GEMM2, combine).  NULL entries are
- * skipped; the registration is consumed by that one call.
+ * forward: x permute + plan, GEMM1, GEMM2, combine; a stage that launches
+ * nothing, such as the plan of a small streaming layer, still records its
+ * event).  NULL entries are skipped; the registration is consumed by that
+ * one call.  Fence-free events (hipEventDisableSystemFence) keep the markers
+ * from adding cache flushes between the stages.
  */
 int lq_moe_profile_events(void *const *events, int n_events);
 
