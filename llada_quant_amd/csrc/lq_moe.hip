@@ -196,9 +196,11 @@ struct WChunk<8> {
 // multiple of 128, lanes past K hold zero codes (out-of-range loads), which
 // dequantize to +0 and meet finite token values; the folded form never sees
 // such a chunk (it needs group lengths that are multiples of 128).
-template <int BITS, bool FOLDED, bool FAST, int NRT, int NT>
-__device__ __forceinline__ void chunk_mfma(const WChunk<BITS> (&w)[NT], const float (&sc)[NT],
-                                           const unsigned char *buf, int lc, int lg, floatx4 (&tot)[NRT][NT]) {
+// afrag(rt, s): this lane's A fragment (8 bf16 of row rt*16 + lc, K piece
+// 4*lg + s of the chunk, K-slot order) from LDS
+template <int BITS, bool FOLDED, bool FAST, int NRT, int NT, class AFrag>
+__device__ __forceinline__ void chunk_mfma_f(const WChunk<BITS> (&w)[NT], const float (&sc)[NT], AFrag afrag,
+                                             floatx4 (&tot)[NRT][NT]) {
   const uint4 ones4 = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);  // bf16 1.0
   floatx4 acc[NRT][NT];
   floatx4 xs[NRT];
@@ -228,9 +230,7 @@ __device__ __forceinline__ void chunk_mfma(const WChunk<BITS> (&w)[NT], const fl
     }
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt) {
-      // row rt*16 + lc (its low 4 bits are lc), K piece 4*lg + s of this 128-wide chunk
-      const uint4 af = *reinterpret_cast<const uint4 *>(buf + (rt * 16 + lc) * kRowBytes +
-                                                        16 * ((4 * lg + s) ^ lc));
+      const uint4 af = afrag(rt, s);
       if constexpr (!FOLDED) {
 #pragma unroll
         for (int c = 0; c < NT; ++c)
@@ -258,6 +258,18 @@ __device__ __forceinline__ void chunk_mfma(const WChunk<BITS> (&w)[NT], const fl
         for (int j = 0; j < 4; ++j)
           tot[rt][c][j] = fmaf(sc[c], fmaf(-kBias, xs[rt][j], acc[rt][c][j]), tot[rt][c][j]);
   }
+}
+
+template <int BITS, bool FOLDED, bool FAST, int NRT, int NT>
+__device__ __forceinline__ void chunk_mfma(const WChunk<BITS> (&w)[NT], const float (&sc)[NT],
+                                           const unsigned char *buf, int lc, int lg, floatx4 (&tot)[NRT][NT]) {
+  chunk_mfma_f<BITS, FOLDED, FAST, NRT, NT>(
+      w, sc,
+      [&](int rt, int s) __attribute__((always_inline)) {
+        // row rt*16 + lc (its low 4 bits are lc), K piece 4*lg + s of this 128-wide chunk
+        return *reinterpret_cast<const uint4 *>(buf + (rt * 16 + lc) * kRowBytes + 16 * ((4 * lg + s) ^ lc));
+      },
+      tot);
 }
 
 // ---------------------------------------------------------------------------
@@ -591,6 +603,8 @@ __device__ void wave0_exclusive_scan(const int *in, int *out, int E, int *total)
 // and up tiles need not meet in one wave.
 // ---------------------------------------------------------------------------
 
+typedef const __attribute__((address_space(3))) unsigned char *lds_cptr;  // LDS byte pointer
+
 constexpr int kSWaves = 12;
 constexpr int kSThreads = 64 * kSWaves;
 
@@ -612,15 +626,19 @@ __device__ __forceinline__ uint16_t swiglu_bf16(float g, float u) {
 // Token rows [row0, row0 + rows) of one block, whole K, into LDS chunk tiles.
 // G1 copies x into K-slot order; G2 builds act = SwiGLU(g, u) from
 // the gate / up pre-activations and permutes it into K-slot order.
-template <bool FIRST>
+// issue_codes() runs right after the last batch of row loads is issued:
+// the load counter retires in order, so rows loaded before the first codes
+// are written to LDS without waiting for those codes.  A block of <= 32
+// rows with K <= 12 * 128 (G1) or 6 * 128 (G2) is one batch.
+template <bool FIRST, class IssueCodes>
 __device__ __forceinline__ void stage_block(const MoeArgs &a, int row0, int rows, const int32_t *rtok,
-                                            unsigned char *lds) {
+                                            unsigned char *lds, IssueCodes issue_codes) {
   const int K = FIRST ? a.H : a.I;
   const int nk = K / kKC;
   const int per_row = nk * 16;  // 16-byte pieces (8 values) per row
   const int total = rows * per_row;
-  constexpr int kBatch = FIRST ? 8 : 4;
-  for (int q0 = 0; q0 < total; q0 += kBatch * kSThreads) {
+  constexpr int kBatch = FIRST ? 12 : 6;
+  auto batch = [&](int q0, auto first_tag) __attribute__((always_inline)) {
     u32x4 v[kBatch];
     u32x4 vu[FIRST ? 1 : kBatch];
     int dst[kBatch];
@@ -643,6 +661,11 @@ __device__ __forceinline__ void stage_block(const MoeArgs &a, int row0, int rows
       }
       dst[i] = q0i < total ? (c * kRowsMax + r) * kRowBytes + 16 * (pc ^ (r & 15)) : -1;
     }
+    if constexpr (decltype(first_tag)::value) {
+      __builtin_amdgcn_sched_barrier(0);
+      issue_codes();
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) {
       u32x4 o = v[i];
@@ -663,6 +686,28 @@ __device__ __forceinline__ void stage_block(const MoeArgs &a, int row0, int rows
       }
       if (dst[i] >= 0) *reinterpret_cast<u32x4 *>(lds + dst[i]) = o;
     }
+  };
+  // earlier batches (large blocks only) first, so no row load is issued
+  // after the codes
+  const int nbatch = (total + kBatch * kSThreads - 1) / (kBatch * kSThreads);
+  for (int bi = 0; bi + 1 < nbatch; ++bi) batch(bi * kBatch * kSThreads, std::false_type{});
+  batch((nbatch - 1) * kBatch * kSThreads, std::true_type{});
+}
+
+// the steps of one run of KD chunks, unrolled (step(integral_constant<d>))
+template <int KD, class Step>
+__device__ __forceinline__ void run_steps(Step step) {
+  step(std::integral_constant<int, 0>{});
+  step(std::integral_constant<int, 1>{});
+  if constexpr (KD > 2) {
+    step(std::integral_constant<int, 2>{});
+    step(std::integral_constant<int, 3>{});
+  }
+  if constexpr (KD > 4) {
+    step(std::integral_constant<int, 4>{});
+    step(std::integral_constant<int, 5>{});
+    step(std::integral_constant<int, 6>{});
+    step(std::integral_constant<int, 7>{});
   }
 }
 
@@ -676,14 +721,15 @@ __device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, 
   const int f0 = u_first + wave;
   const int nunits = f0 < u_end ? (u_end - f0 + kSWaves - 1) / kSWaves : 0;
   const int K = FIRST ? a.H : a.I;
-  const int nk = K / kKC;  // a multiple of KD (host-checked)
-  const int nsteps = nunits * nk;
+  const int nk = K / kKC;  // a multiple of KD (host-checked), so a run never crosses a unit
+  const int nruns = nunits * (nk / KD);
   const int rowbytes = BITS == 4 ? (K >> 1) : K;
   const int ng = FIRST ? a.ng1 : a.ng2;
   const int cpg = (FIRST ? a.g1 : a.g2) / kKC;  // chunks per group (group lengths are multiples of 128)
   const int nrows_w = FIRST ? 2 * a.I : a.H;
   constexpr int kLaneBytes = BITS == 4 ? 16 : 32;
   constexpr int kChunkBytes = BITS == 4 ? 64 : 128;
+  constexpr int kChunkLds = kRowsMax * kRowBytes;  // one staged chunk of the block's rows
   const __amdgpu_buffer_rsrc_t wrsrc =
       make_rsrc((FIRST ? a.q1 : a.q2) + static_cast<int64_t>(e) * nrows_w * rowbytes,
                 static_cast<int64_t>(nrows_w) * rowbytes);
@@ -692,52 +738,65 @@ __device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, 
   const __amdgpu_buffer_rsrc_t empty = make_rsrc(a.out, 0);
   const int wvoff = lc * rowbytes + kLaneBytes * lg;  // this lane's codes within a tile chunk
   const int svoff = lc * ng * 4;
+  const int sqvoff = lc * ng * 4 + 16 * lg;           // SQ: this lane's 4 scales within a tile
 
-  // load cursor (scalar registers, advanced incrementally): the codes and
-  // scale offsets of the next chunk to load, its chunk index within the unit
-  // and the loads left; after the wave's last chunk both descriptors become
-  // the empty one.
+  // Load cursor (scalar registers), one run of KD chunks ahead of the
+  // compute: the unit lu and first chunk lc0 of the run being loaded, the
+  // codes offset wso of its first chunk (chunk d at wso + d * kChunkBytes,
+  // an immediate offset), the unit's scale offset suo, and the runs left;
+  // after the wave's last run both descriptors become the empty one, so
+  // every step issues the same loads and the load counter stays static.
   // SQ (group length 128, at most 16 chunks): instead of one scale load per
   // chunk, lane (r, g) loads the scales of groups 4g .. 4g+3 of its tile row
-  // r once per unit (one dwordx4, issued in the first step of every run of
-  // KD loads -- from the empty descriptor when that run does not start a
-  // unit); the scale of chunk c then comes from lane (r, c / 4) by
-  // ds_bpermute.
-  __amdgpu_buffer_rsrc_t rw = nsteps > 0 ? wrsrc : empty, rs = nsteps > 0 ? srsrc : empty;
-  int lu = f0;                                  // unit of the next load
-  int lcur = 0, lgrp = 0;                       // its chunk, and chunk within the group
-  int wso = 16 * lu * rowbytes;                 // codes offset of that chunk
-  int sso = 16 * lu * ng * 4;                   // scale offset of that chunk's group
-  int left = nsteps;
+  // r once per unit (one dwordx4 in the first step of a run, from the empty
+  // descriptor when the run does not start a unit); the scale of chunk c
+  // then comes from lane (r, c / 4) by ds_bpermute.  Otherwise every chunk
+  // loads its scale (sso, lgrp: the next chunk's scale offset and its
+  // position within its group).
+  __amdgpu_buffer_rsrc_t rw = nruns > 0 ? wrsrc : empty, rs = nruns > 0 ? srsrc : empty;
+  int lu = f0, lc0 = 0;
+  int wso = 16 * lu * rowbytes;
+  int suo = 16 * lu * ng * 4;
+  int sso = suo, lgrp = 0;
+  int left = nruns;
   u32x4 sq_cur = u32x4{0, 0, 0, 0}, sq_next = u32x4{0, 0, 0, 0};
-  const int sqvoff = lc * ng * 4 + 16 * lg;     // SQ: this lane's 4 scales within a tile
   auto load_sq = [&](u32x4 &dst) __attribute__((always_inline)) {
-    dst = __builtin_amdgcn_raw_buffer_load_b128(lcur == 0 ? rs : empty, sqvoff, lcur == 0 ? sso : 0, 0);
+    dst = __builtin_amdgcn_raw_buffer_load_b128(lc0 == 0 ? rs : empty, sqvoff, lc0 == 0 ? suo : 0, 0);
   };
-  auto load_w = [&](WChunk<BITS>(&w)[1], float(&sc)[1]) __attribute__((always_inline)) {
+  auto load_w = [&](auto d_tag, WChunk<BITS>(&w)[1], float(&sc)[1]) __attribute__((always_inline)) {
+    constexpr int d = decltype(d_tag)::value;
     if constexpr (BITS == 4) {
-      w[0].v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, wvoff, wso, 0));
+      w[0].v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, wvoff + d * kChunkBytes, wso, 0));
     } else {
-      w[0].v0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, wvoff, wso, 0));
-      w[0].v1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, wvoff + 16, wso, 0));
+      w[0].v0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, wvoff + d * kChunkBytes, wso, 0));
+      w[0].v1 =
+          __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, wvoff + d * kChunkBytes + 16, wso, 0));
     }
-    if constexpr (!SQ) sc[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, svoff, sso, 0));
-    wso += kChunkBytes;
-    if (++lgrp == cpg) {
-      lgrp = 0;
-      sso += 4;
+    if constexpr (!SQ) {
+      sc[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, svoff, sso, 0));
+      if (++lgrp == cpg) {
+        lgrp = 0;
+        sso += 4;
+      }
     }
-    if (++lcur == nk) {
-      lcur = 0;
-      lgrp = 0;
+  };
+  // advance the load cursor past the run just loaded
+  auto next_run = [&]() __attribute__((always_inline)) {
+    lc0 += KD;
+    wso += KD * kChunkBytes;
+    if (lc0 == nk) {
+      lc0 = 0;
       lu += kSWaves;
       wso = 16 * lu * rowbytes;
-      sso = 16 * lu * ng * 4;
+      suo = 16 * lu * ng * 4;
+      sso = suo;
+      lgrp = 0;
     }
     if (--left == 0) {
       rw = empty;
       rs = empty;
       wso = 0;
+      suo = 0;
       sso = 0;
     }
   };
@@ -766,68 +825,91 @@ __device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, 
     for (int rt = 0; rt < NRT; ++rt) tot[rt][0] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
   };
 
-  // KD steps of codes in flight; step i consumes slot i % KD and refills it
-  // with step i + KD (loads past the wave's last step go through the empty
-  // descriptor, so every step issues the same loads)
+  // KD chunks of codes in flight; step d of a run consumes slot d and
+  // refills it with chunk d of the next run
   WChunk<BITS> wb[KD][1];
   float sb[KD][1];
-#pragma unroll
-  for (int d = 0; d < KD; ++d) {
-    if constexpr (SQ) {
-      if (d == 0) load_sq(sq_cur);
-    }
-    load_w(wb[d], sb[d]);
-    __builtin_amdgcn_sched_barrier(0);
-  }
   // the block's token rows are staged while the first codes are in flight
   __syncthreads();  // the previous block's rows are no longer read
-  stage_block<FIRST>(a, row0, rows, rtok, lds);
+  stage_block<FIRST>(a, row0, rows, rtok, lds, [&]() __attribute__((always_inline)) {
+    if constexpr (SQ) load_sq(sq_cur);
+    run_steps<KD>([&](auto d_tag) __attribute__((always_inline)) {
+      constexpr int d = decltype(d_tag)::value;
+      load_w(d_tag, wb[d], sb[d]);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    next_run();
+  });
   __syncthreads();
-  if (nsteps == 0) return;
-  int cu = f0, cc = 0;  // compute cursor: unit, first chunk of the current KD steps
-  auto step = [&](auto d_tag) __attribute__((always_inline)) {
-    constexpr int d = decltype(d_tag)::value;
-    const unsigned char *buf = lds + (cc + d) * (kRowsMax * kRowBytes);
-    if constexpr (SQ) {
-      // chunk cc + d (cc is a multiple of 4): component d % 4 of lane (r, (cc + d) / 4)
-      const int src = (lc + 16 * ((cc + d) >> 2)) << 2;
-      sb[d][0] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(sq_cur[d & 3])));
-    }
-    if constexpr (FOLDED) {
-      chunk_mfma<BITS, FOLDED, true, NRT, 1>(wb[d], sb[d], buf, lc, lg, tot);
-    } else {
-      if (__all(dq_fast_ok(sb[d][0])))
-        chunk_mfma<BITS, FOLDED, true, NRT, 1>(wb[d], sb[d], buf, lc, lg, tot);
-      else
-        chunk_mfma<BITS, FOLDED, false, NRT, 1>(wb[d], sb[d], buf, lc, lg, tot);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (SQ) {
-      if (d == 0) load_sq(sq_next);
-    }
-    load_w(wb[d], sb[d]);
-    __builtin_amdgcn_sched_barrier(0);
+  if (nruns == 0) return;
+  // SQ: whether every scale of the current unit takes the fast dequant
+  // (decided per unit, so a run is all fast or all exact-slow); scale slots
+  // past the row's last group are not looked at
+  auto unit_fast = [&]() __attribute__((always_inline)) {
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ok = ok && (4 * lg + i >= ng || dq_fast_ok(__uint_as_float(sq_cur[i])));
+    return __all(ok) != 0;
   };
-  // nk is a multiple of KD, so a unit ends only after the last step of a block
-  for (int s0 = 0; s0 < nsteps; s0 += KD) {
-    step(std::integral_constant<int, 0>{});
-    step(std::integral_constant<int, 1>{});
-    if constexpr (KD > 2) {
-      step(std::integral_constant<int, 2>{});
-      step(std::integral_constant<int, 3>{});
+  bool fast_unit = SQ && !FOLDED ? unit_fast() : true;
+  // LDS address of this lane's A fragment for K piece 4*lg + s of chunk 0,
+  // row lc (the XOR swizzle of the staging)
+  const lds_cptr lbase = (lds_cptr)(lds);
+  int aoff[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) aoff[s] = lc * kRowBytes + 16 * ((4 * lg + s) ^ lc);
+  int cu = f0, cc = 0;  // compute cursor: unit, first chunk of the current run
+  for (int r = 0; r < nruns; ++r) {
+    // the run's A addresses, computed once and kept opaque so every step
+    // and row tile reaches its fragment through the instruction's
+    // immediate offset (d * kChunkLds + rt * 16 * kRowBytes)
+    lds_cptr ab[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      ab[s] = lbase + (aoff[s] + cc * kChunkLds);
+      asm volatile("" : "+v"(ab[s]));
     }
-    if constexpr (KD > 4) {
-      step(std::integral_constant<int, 4>{});
-      step(std::integral_constant<int, 5>{});
-      step(std::integral_constant<int, 6>{});
-      step(std::integral_constant<int, 7>{});
-    }
+    int sqa = (lc + 16 * (cc >> 2)) << 2;  // SQ: source lane of the run's first chunk, in bytes
+    asm volatile("" : "+v"(sqa));
+    // the fast / exact-slow choice is made per step but from a per-unit
+    // flag, so both paths rejoin before the step's loads (one register
+    // assignment for the codes in flight)
+    run_steps<KD>([&](auto d_tag) __attribute__((always_inline)) {
+      constexpr int d = decltype(d_tag)::value;
+      auto afrag = [&](int rt, int s) __attribute__((always_inline)) {
+        const u32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4 *>(
+            ab[s] + (d * kChunkLds + rt * 16 * kRowBytes));
+        return make_uint4(v[0], v[1], v[2], v[3]);
+      };
+      if constexpr (SQ) {
+        // chunk cc + d (cc is a multiple of 4): component d % 4 of lane (r, (cc + d) / 4)
+        sb[d][0] = __int_as_float(__builtin_amdgcn_ds_bpermute(sqa + 64 * (d >> 2), static_cast<int>(sq_cur[d & 3])));
+      }
+      if constexpr (FOLDED) {
+        chunk_mfma_f<BITS, FOLDED, true, NRT, 1>(wb[d], sb[d], afrag, tot);
+      } else {
+        if (SQ ? fast_unit : __all(dq_fast_ok(sb[d][0])) != 0)
+          chunk_mfma_f<BITS, FOLDED, true, NRT, 1>(wb[d], sb[d], afrag, tot);
+        else
+          chunk_mfma_f<BITS, FOLDED, false, NRT, 1>(wb[d], sb[d], afrag, tot);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (SQ) {
+        if (d == 0) load_sq(sq_next);
+      }
+      load_w(d_tag, wb[d], sb[d]);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    next_run();
     cc += KD;
     if (cc == nk) {
       epilogue(cu);
       cc = 0;
       cu += kSWaves;
-      if constexpr (SQ) sq_cur = sq_next;
+      if constexpr (SQ) {
+        sq_cur = sq_next;
+        if constexpr (!FOLDED) fast_unit = unit_fast();
+      }
     }
   }
 }
@@ -841,9 +923,16 @@ __device__ __forceinline__ void stream_block(const MoeArgs &a, int e, int row0, 
     stream_units<BITS, FOLDED, FIRST, 2, KD, SQ>(a, e, row0, rows, rtok, rasg, u_first, u_end, lds);
 }
 
-// CU c of G and its share of nb blocks: with nb <= G, CUs
-// [ceil(b G / nb), ceil((b+1) G / nb)) share block b, CU c taking units
-// [i upb / m, (i+1) upb / m) of it; returns false for a CU without a block
+// Workgroup g of a grid of G runs on XCD g % 8.  Its XCD-major slot
+// (g % 8) * (G / 8) + g / 8 numbers the workgroups of one XCD
+// consecutively, so the CUs that share a block -- which stage the same
+// token rows -- and the blocks of one expert -- which stream the same
+// weights at about the same time -- meet in one L2.
+__device__ __forceinline__ int xcd_slot(int g, int G) { return G % 8 ? g : (g % 8) * (G / 8) + g / 8; }
+
+// Slot c of G and its share of nb blocks: with nb <= G, slots
+// [ceil(b G / nb), ceil((b+1) G / nb)) share block b, slot c taking units
+// [i upb / m, (i+1) upb / m) of it; returns false for a slot without a block
 __device__ __forceinline__ bool cu_share(int c, int G, int nb, int upb, int &b, int &ub, int &ue) {
   b = static_cast<int>(static_cast<int64_t>(c) * nb / G);
   if (b >= nb) return false;
@@ -860,71 +949,109 @@ __device__ __forceinline__ bool cu_share(int c, int G, int nb, int upb, int &b, 
 // output -- the same per-expert counts and offsets, the same expert-major
 // blocks of <= 32 rows, and the block's assignments in ascending flat index
 // (plan_kernel's stable order), so the sorted row numbers G1 writes and G2
-// reads agree.  Fills rtok / rasg (token and assignment of each row) and
-// returns false when the CU has no block.
+// reads agree.  One barrier: after the ids are counted, every wave scans the
+// counts in registers, finds its block and compacts the block's assignments
+// itself (all waves write the same values into rtok / rasg; the barrier that
+// opens the staging orders those writes before any read).  Fills rtok / rasg
+// (token and assignment of each row) and returns false when the CU has no
+// block.
 constexpr int kPlanMaxN = 2048;
 __device__ __forceinline__ bool block_plan(const MoeArgs &a, int upb, int &e, int &row0, int &rows, int &ub,
                                            int &ue, int32_t *rtok, int32_t *rasg) {
   __shared__ int cnt[kMaxExperts];
-  __shared__ int off[kMaxExperts];
-  __shared__ int nbk[kMaxExperts];
-  __shared__ int nbs[kMaxExperts + 1];
-  __shared__ int wcount[kSWaves];
-  __shared__ int total;
+  __shared__ uint16_t ids_l[kPlanMaxN];  // expert of each assignment (0xFFFF: none)
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
   const int lane = tid & 63;
   const int N = static_cast<int>(a.T * a.k);
   const int E = a.E;
+  // the ids are read once, all in one round trip
+  constexpr int kIdsPerThread = (kPlanMaxN + kSThreads - 1) / kSThreads;
+  int idr[kIdsPerThread];
+#pragma unroll
+  for (int j = 0; j < kIdsPerThread; ++j) {
+    const int i = j * kSThreads + tid;
+    idr[j] = i < N ? a.ids[i] : -1;
+  }
   for (int i = tid; i < E; i += kSThreads) cnt[i] = 0;
   __syncthreads();
-  for (int i = tid; i < N; i += kSThreads) {
-    const int id = a.ids[i];
-    if (id >= 0 && id < E) atomicAdd(&cnt[id], 1);
+#pragma unroll
+  for (int j = 0; j < kIdsPerThread; ++j) {
+    const int i = j * kSThreads + tid;
+    const bool ok = idr[j] >= 0 && idr[j] < E;
+    if (i < N) ids_l[i] = ok ? static_cast<uint16_t>(idr[j]) : uint16_t{0xFFFF};
+    if (ok) atomicAdd(&cnt[idr[j]], 1);
   }
   __syncthreads();
-  if (wave == 0) {
-    wave0_exclusive_scan(cnt, off, E, &total);
-  } else if (wave == 1) {
-    // blocks per expert and their scan (wave 1 writes nbk, then scans it)
-    for (int i = lane; i < E; i += 64) nbk[i] = (cnt[i] + kRowsMax - 1) / kRowsMax;
-    __builtin_amdgcn_wave_barrier();
-    wave0_exclusive_scan(nbk, nbs, E, &nbs[E]);
+  // lane l: experts 4l .. 4l+3, their rows and row blocks, and the
+  // exclusive prefix of both over the lanes
+  int c[4], nbk[4], csum = 0, bsum = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ex = 4 * lane + i;
+    c[i] = ex < E ? cnt[ex] : 0;
+    nbk[i] = (c[i] + kRowsMax - 1) / kRowsMax;
+    csum += c[i];
+    bsum += nbk[i];
   }
-  __syncthreads();
-  const int nb = nbs[E];
+  int cinc = csum, binc = bsum;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int yc = __shfl_up(cinc, o, 64);
+    const int yb = __shfl_up(binc, o, 64);
+    if (lane >= o) {
+      cinc += yc;
+      binc += yb;
+    }
+  }
+  const int nb = __builtin_amdgcn_readlane(binc, 63);
   int b;
-  if (!cu_share(blockIdx.x, gridDim.x, nb, upb, b, ub, ue)) return false;
-  int lo = 0, hi = E;  // largest expert with nbs[expert] <= b
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if (nbs[mid] <= b) lo = mid;
-    else hi = mid;
+  if (!cu_share(xcd_slot(blockIdx.x, gridDim.x), gridDim.x, nb, upb, b, ub, ue)) return false;
+  // the lane whose experts hold block b, then the expert within it
+  const int bex = binc - bsum;
+  const int owner = static_cast<int>(__builtin_ctzll(__ballot(bex <= b && b < binc)));
+  int fe = 0, fblk = 0, foff = 0, fcnt = 0;
+  int eb = bex, eo = cinc - csum;
+  bool found = false;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (!found && b < eb + nbk[i]) {
+      found = true;
+      fe = 4 * lane + i;
+      fblk = eb;
+      foff = eo;
+      fcnt = c[i];
+    }
+    eb += nbk[i];
+    eo += c[i];
   }
-  e = __builtin_amdgcn_readfirstlane(lo);
-  const int first = (b - nbs[e]) * kRowsMax;  // rank of the block's first row within expert e
-  rows = __builtin_amdgcn_readfirstlane(min(kRowsMax, cnt[e] - first));
-  row0 = __builtin_amdgcn_readfirstlane(off[e] + first);
+  e = __builtin_amdgcn_readlane(fe, owner);
+  const int first = (b - __builtin_amdgcn_readlane(fblk, owner)) * kRowsMax;  // rank of the block's first row
+  rows = min(kRowsMax, __builtin_amdgcn_readlane(fcnt, owner) - first);
+  row0 = __builtin_amdgcn_readlane(foff, owner) + first;
   // stable compaction of expert e's assignments, keeping ranks [first, first + rows)
   const unsigned long long lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  const int last = first + rows;
   int run = 0;
-  for (int c0 = 0; c0 < N; c0 += kSThreads) {
-    const int i = c0 + tid;
-    const bool hit = i < N && a.ids[i] == e;
-    const unsigned long long bal = __ballot(hit);
-    if (lane == 0) wcount[wave] = __popcll(bal);
-    __syncthreads();
-    int before = run;
-    for (int w = 0; w < wave; ++w) before += wcount[w];
-    const int rank = before + __popcll(bal & lt);
-    if (hit && rank >= first && rank < first + rows) {
-      rasg[rank - first] = i;
-      rtok[rank - first] = i / a.k;
+  for (int c0 = 0; c0 < N && run < last; c0 += 256) {
+    int idv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = c0 + 64 * j + lane;
+      idv[j] = i < N ? ids_l[i] : 0xFFFF;
     }
-    for (int w = 0; w < kSWaves; ++w) run += wcount[w];
-    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = c0 + 64 * j + lane;
+      const bool hit = idv[j] == e;
+      const unsigned long long bal = __ballot(hit);
+      const int rank = run + __popcll(bal & lt);
+      if (hit && rank >= first && rank < last) {
+        rasg[rank - first] = i;
+        rtok[rank - first] = i / a.k;
+      }
+      run += __popcll(bal);
+    }
   }
-  __syncthreads();
   return true;
 }
 
@@ -939,7 +1066,7 @@ __global__ __launch_bounds__(kSThreads, 1) void moe_stream_kernel(MoeArgs a) {
     stream_block<BITS, FOLDED, FIRST, KD, SQ>(a, e, row0, rows, rtok, rasg, ub, ue, slds);
   } else {
     const int nb = __builtin_amdgcn_readfirstlane(a.hdr->n_blk);
-    const int G = gridDim.x, c = blockIdx.x;
+    const int G = gridDim.x, c = xcd_slot(blockIdx.x, gridDim.x);
     auto run_block = [&](int b, int ub, int ue) __attribute__((always_inline)) {
       const int4 bi = a.blocks[b];
       const int e = __builtin_amdgcn_readfirstlane(bi.x);
@@ -1261,9 +1388,6 @@ int launch_stream_kd(const MoeArgs &a, hipStream_t st) {
   return check_launch(FIRST ? "moe_stream_gemm1" : "moe_stream_gemm2");
 }
 
-// chunks in flight per wave: 8 KB of codes where K allows (INT4: 8 x 1 KB,
-// INT8: 4 x 2 KB), half that otherwise; the folded INT4 form keeps 4 (its
-// extra accumulators leave no registers for 8)
 template <int BITS, bool FOLDED, bool FIRST, int KD, bool SQ>
 int launch_stream_plan(const MoeArgs &a, hipStream_t st, bool inplan) {
   return inplan ? launch_stream_kd<BITS, FOLDED, FIRST, KD, SQ, true>(a, st)
