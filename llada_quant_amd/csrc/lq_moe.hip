@@ -112,6 +112,19 @@ __device__ __forceinline__ uint32_t cvt2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2){lo, hi}, bf16x2));
 }
 
+// SwiGLU of gate / up values that are already bf16 (held as floats), in
+// the reference op order (INFERENCE_REPO_CHANGES.md:296-309): silu in fp32,
+// rounded to bf16, times up, rounded to bf16.  exp and the reciprocal are
+// the hardware's (v_exp_f32, v_rcp_f32), so silu is within two fp32 ulps of
+// g / (1 + e^-g) before its rounding; both GEMM families use these, so
+// they agree bit for bit.
+__device__ __forceinline__ float silu_f32(float gb) { return gb * __builtin_amdgcn_rcpf(1.0f + __expf(-gb)); }
+// two features at once: g0/u0 -> low half, g1/u1 -> high half
+__device__ __forceinline__ uint32_t swiglu_pk(float g0, float g1, float u0, float u1) {
+  const uint32_t sb = cvt2(silu_f32(g0), silu_f32(g1));
+  return cvt2(__uint_as_float(sb << 16) * u0, __uint_as_float(sb & 0xFFFF0000u) * u1);
+}
+
 // INT4 folded: 8 nibbles of w -> bf16(128 + (q + 8)) = 136 + q, exact; (q ^ 8) is q + 8
 __device__ __forceinline__ uint4 b_int4_folded(uint32_t w) {
   const uint32_t v = w ^ 0x88888888u;
@@ -472,8 +485,7 @@ __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, in
         if (m < rows) {
           const float gb = bf16_round(tot[rt][0][j]);
           const float ub = bf16_round(tot[rt][1][j]);
-          const float sb16 = bf16_round(gb / (1.0f + __expf(-gb)));
-          a.act[static_cast<int64_t>(row0 + m) * a.I + f] = f32_to_bf16_bits(sb16 * ub);
+          a.act[static_cast<int64_t>(row0 + m) * a.I + f] = static_cast<uint16_t>(swiglu_pk(gb, 0.0f, ub, 0.0f));
         }
       }
   } else {
@@ -608,20 +620,16 @@ typedef const __attribute__((address_space(3))) unsigned char *lds_cptr;  // LDS
 constexpr int kSWaves = 12;
 constexpr int kSThreads = 64 * kSWaves;
 
-// LDS bytes of the streaming kernels for reduction length K (token rows of
-// one block for the whole K)
-inline size_t stream_lds_bytes(int K) { return static_cast<size_t>(K) * kRowsMax * 2; }
+// partial accumulators one wave hands to the next (one slot per wave: its
+// tile's 32 x 16 fp32 values)
+constexpr int kSlotBytes = kRowsMax * 16 * 4;
+// LDS bytes of the streaming kernels for reduction length K: the token rows
+// of one block for the whole K, then the hand-over slots
+__host__ __device__ inline size_t stream_rows_bytes(int K) { return static_cast<size_t>(K) * kRowsMax * 2; }
+inline size_t stream_lds_bytes(int K) { return stream_rows_bytes(K) + static_cast<size_t>(kSWaves) * kSlotBytes; }
 // upper bound of the static LDS of the streaming kernels (block_plan's tables)
 constexpr size_t kStaticLds = 8192;
 
-// reference op order (INFERENCE_REPO_CHANGES.md:296-309): g, u -> bf16;
-// silu in fp32 -> bf16; bf16 product
-__device__ __forceinline__ uint16_t swiglu_bf16(float g, float u) {
-  const float gb = bf16_round(g);
-  const float ub = bf16_round(u);
-  const float sb16 = bf16_round(gb / (1.0f + __expf(-gb)));
-  return f32_to_bf16_bits(sb16 * ub);
-}
 
 // Token rows [row0, row0 + rows) of one block, whole K, into LDS chunk tiles.
 // G1 copies x into K-slot order; G2 builds act = SwiGLU(g, u) from
@@ -673,13 +681,13 @@ __device__ __forceinline__ void stage_block(const MoeArgs &a, int row0, int rows
         const uint4 perm = permute_kslots(make_uint4(o[0], o[1], o[2], o[3]));  // x into K-slot order
         o = u32x4{perm.x, perm.y, perm.z, perm.w};
       } else {
+        // gate / up were stored as bf16, so they enter SwiGLU unrounded
         uint32_t p[4];
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
           const uint32_t gw = v[i][h], uw = vu[i][h];
-          const uint16_t lo = swiglu_bf16(__uint_as_float(gw << 16), __uint_as_float(uw << 16));
-          const uint16_t hi = swiglu_bf16(__uint_as_float(gw & 0xFFFF0000u), __uint_as_float(uw & 0xFFFF0000u));
-          p[h] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+          p[h] = swiglu_pk(__uint_as_float(gw << 16), __uint_as_float(gw & 0xFFFF0000u), __uint_as_float(uw << 16),
+                           __uint_as_float(uw & 0xFFFF0000u));
         }
         const uint4 perm = permute_kslots(make_uint4(p[0], p[1], p[2], p[3]));
         o = u32x4{perm.x, perm.y, perm.z, perm.w};
@@ -711,18 +719,65 @@ __device__ __forceinline__ void run_steps(Step step) {
   }
 }
 
+// The units [u_first, u_end) of one CU over its waves: F = nu / W full
+// rounds, wave w taking units u_first + w + W i (i < F), then the T = nu % W
+// left-over units.  A unit is rpu = nk / KD runs of KD chunks.  When rpu is
+// even, each left-over unit t is cut in half so the waves finish together:
+// wave t works its head (first rpu / 2 runs) before anything else and hands
+// the partial sums over through LDS; wave (T + t) % W continues from them
+// after its full rounds -- so every unit still sums its chunks in order, as
+// the general kernels do, and the two families agree bit for bit.
+// Otherwise wave w takes left-over unit t = w whole.  Per wave that makes up
+// to three segments of runs: the head (S1), the full rounds (S2, unit
+// stride W) and the left-over unit or tail (S3).
 template <int BITS, bool FOLDED, bool FIRST, int NRT, int KD, bool SQ>
 __device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, int rows, const int32_t *rtok,
                                              const int32_t *rasg, int u_first, int u_end, unsigned char *lds) {
+  __shared__ int hand_flag[kSWaves];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int lc = lane & 15;
   const int lg = lane >> 4;
-  const int f0 = u_first + wave;
-  const int nunits = f0 < u_end ? (u_end - f0 + kSWaves - 1) / kSWaves : 0;
   const int K = FIRST ? a.H : a.I;
   const int nk = K / kKC;  // a multiple of KD (host-checked), so a run never crosses a unit
-  const int nruns = nunits * (nk / KD);
+  const int rpu = nk / KD;  // runs per unit
+  const int nu = u_end - u_first;
+  const int F = nu / kSWaves, T = nu - F * kSWaves;
+  const bool split = T > 0 && rpu % 2 == 0;
+  const int half = rpu / 2;
+  const int ut = u_first + F * kSWaves;  // first left-over unit
+  const int t3 = (wave - T + kSWaves) % kSWaves;  // split: the left-over unit whose tail this wave works
+  const int n1 = split && wave < T ? half : 0;
+  const int n2 = F * rpu;
+  const int n3 = split ? (t3 < T ? half : 0) : (wave < T ? rpu : 0);
+  const int u3 = split ? ut + t3 : ut + wave;
+  const int c3 = split ? half * KD : 0;
+  const int nruns = n1 + n2 + n3;
+  // Move a cursor (segment index, unit, first chunk, runs left in the
+  // segment, unit stride) to the first non-empty segment after `from`
+  // (-1: the first one).  Explicit branches with the segments' own values:
+  // a select over the segment index would become a table in private memory.
+  auto enter = [&](int from, int &sg, int &u, int &c, int &n, int &stride) __attribute__((always_inline)) {
+    if (from < 0 && n1 > 0) {
+      sg = 0;
+      u = ut + wave;
+      c = 0;
+      n = n1;
+      stride = 1;
+    } else if (from < 1 && n2 > 0) {
+      sg = 1;
+      u = u_first + wave;
+      c = 0;
+      n = n2;
+      stride = kSWaves;
+    } else {
+      sg = 2;
+      u = u3;
+      c = c3;
+      n = n3;
+      stride = 1;
+    }
+  };
   const int rowbytes = BITS == 4 ? (K >> 1) : K;
   const int ng = FIRST ? a.ng1 : a.ng2;
   const int cpg = (FIRST ? a.g1 : a.g2) / kKC;  // chunks per group (group lengths are multiples of 128)
@@ -739,29 +794,35 @@ __device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, 
   const int wvoff = lc * rowbytes + kLaneBytes * lg;  // this lane's codes within a tile chunk
   const int svoff = lc * ng * 4;
   const int sqvoff = lc * ng * 4 + 16 * lg;           // SQ: this lane's 4 scales within a tile
+  float *slots = reinterpret_cast<float *>(lds + stream_rows_bytes(K));
 
   // Load cursor (scalar registers), one run of KD chunks ahead of the
   // compute: the unit lu and first chunk lc0 of the run being loaded, the
   // codes offset wso of its first chunk (chunk d at wso + d * kChunkBytes,
-  // an immediate offset), the unit's scale offset suo, and the runs left;
+  // an immediate offset), the unit's scale offset suo, the head runs still
+  // to load (seg1; then the cursor jumps to uA / cA), and the runs left;
   // after the wave's last run both descriptors become the empty one, so
   // every step issues the same loads and the load counter stays static.
   // SQ (group length 128, at most 16 chunks): instead of one scale load per
   // chunk, lane (r, g) loads the scales of groups 4g .. 4g+3 of its tile row
-  // r once per unit (one dwordx4 in the first step of a run, from the empty
-  // descriptor when the run does not start a unit); the scale of chunk c
-  // then comes from lane (r, c / 4) by ds_bpermute.  Otherwise every chunk
-  // loads its scale (sso, lgrp: the next chunk's scale offset and its
+  // r once per unit (one dwordx4 in the first step of a run that starts a
+  // unit or follows a jump, else from the empty descriptor); the scale of
+  // chunk c then comes from lane (r, c / 4) by ds_bpermute.  Otherwise every
+  // chunk loads its scale (sso, lgrp: the next chunk's scale offset and its
   // position within its group).
   __amdgpu_buffer_rsrc_t rw = nruns > 0 ? wrsrc : empty, rs = nruns > 0 ? srsrc : empty;
-  int lu = f0, lc0 = 0;
-  int wso = 16 * lu * rowbytes;
+  int lseg, lu, lc0, lseg_left, lstride;
+  enter(-1, lseg, lu, lc0, lseg_left, lstride);
+  int wso = 16 * lu * rowbytes + lc0 * kChunkBytes;
   int suo = 16 * lu * ng * 4;
-  int sso = suo, lgrp = 0;
+  int sso = suo + (lc0 / cpg) * 4, lgrp = lc0 % cpg;
   int left = nruns;
+  bool sq_force = true;
   u32x4 sq_cur = u32x4{0, 0, 0, 0}, sq_next = u32x4{0, 0, 0, 0};
   auto load_sq = [&](u32x4 &dst) __attribute__((always_inline)) {
-    dst = __builtin_amdgcn_raw_buffer_load_b128(lc0 == 0 ? rs : empty, sqvoff, lc0 == 0 ? suo : 0, 0);
+    const bool go = lc0 == 0 || sq_force;
+    dst = __builtin_amdgcn_raw_buffer_load_b128(go ? rs : empty, sqvoff, go ? suo : 0, 0);
+    sq_force = false;
   };
   auto load_w = [&](auto d_tag, WChunk<BITS>(&w)[1], float(&sc)[1]) __attribute__((always_inline)) {
     constexpr int d = decltype(d_tag)::value;
@@ -782,15 +843,24 @@ __device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, 
   };
   // advance the load cursor past the run just loaded
   auto next_run = [&]() __attribute__((always_inline)) {
-    lc0 += KD;
-    wso += KD * kChunkBytes;
-    if (lc0 == nk) {
-      lc0 = 0;
-      lu += kSWaves;
-      wso = 16 * lu * rowbytes;
+    if (--lseg_left == 0 && lseg < 2) {
+      enter(lseg, lseg, lu, lc0, lseg_left, lstride);
+      wso = 16 * lu * rowbytes + lc0 * kChunkBytes;
       suo = 16 * lu * ng * 4;
-      sso = suo;
-      lgrp = 0;
+      sso = suo + (lc0 / cpg) * 4;
+      lgrp = lc0 % cpg;
+      sq_force = true;
+    } else {
+      lc0 += KD;
+      wso += KD * kChunkBytes;
+      if (lc0 == nk) {
+        lc0 = 0;
+        lu += lstride;
+        wso = 16 * lu * rowbytes;
+        suo = 16 * lu * ng * 4;
+        sso = suo;
+        lgrp = 0;
+      }
     }
     if (--left == 0) {
       rw = empty;
@@ -824,13 +894,41 @@ __device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, 
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt) tot[rt][0] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
   };
+  // hand the head's partial sums over (slot and flag of this wave)
+  auto give = [&]() __attribute__((always_inline)) {
+    float *slot = slots + wave * (kSlotBytes / 4);
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        slot[(rt * 4 + j) * 64 + lane] = tot[rt][0][j];
+        tot[rt][0][j] = 0.0f;
+      }
+    __hip_atomic_store(&hand_flag[wave], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  };
+  // continue from the head wave src handed over (it works that head before
+  // anything else, so the wait is short; the cap only bounds the loop)
+  auto take = [&](int src) __attribute__((always_inline)) {
+    for (int spin = 0; spin < (1 << 22); ++spin) {
+      // (one wave-uniform decision, so the loop exit is uniform)
+      const int f = __hip_atomic_load(&hand_flag[src], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (__builtin_amdgcn_readfirstlane(f) != 0) break;
+      __builtin_amdgcn_s_sleep(2);
+    }
+    const float *slot = slots + src * (kSlotBytes / 4);
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) tot[rt][0][j] = slot[(rt * 4 + j) * 64 + lane];
+  };
 
   // KD chunks of codes in flight; step d of a run consumes slot d and
   // refills it with chunk d of the next run
   WChunk<BITS> wb[KD][1];
   float sb[KD][1];
   // the block's token rows are staged while the first codes are in flight
-  __syncthreads();  // the previous block's rows are no longer read
+  __syncthreads();  // the previous block's rows and hand-over slots are no longer read
+  if (lane == 0) hand_flag[wave] = 0;
   stage_block<FIRST>(a, row0, rows, rtok, lds, [&]() __attribute__((always_inline)) {
     if constexpr (SQ) load_sq(sq_cur);
     run_steps<KD>([&](auto d_tag) __attribute__((always_inline)) {
@@ -858,7 +956,11 @@ __device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, 
   int aoff[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) aoff[s] = lc * kRowBytes + 16 * ((4 * lg + s) ^ lc);
-  int cu = f0, cc = 0;  // compute cursor: unit, first chunk of the current run
+  // compute cursor: segment, unit, first chunk of the current run, runs
+  // left in the segment, unit stride
+  int cseg, cu, cc, cseg_left, cstride;
+  enter(-1, cseg, cu, cc, cseg_left, cstride);
+  if (split && cseg == 2) take(t3);
   for (int r = 0; r < nruns; ++r) {
     // the run's A addresses, computed once and kept opaque so every step
     // and row tile reaches its fragment through the instruction's
@@ -902,11 +1004,21 @@ __device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, 
     });
     next_run();
     cc += KD;
-    if (cc == nk) {
+    bool moved = false;
+    if (cc == nk) {  // (a head never completes its unit)
       epilogue(cu);
+      cu += cstride;
       cc = 0;
-      cu += kSWaves;
-      if constexpr (SQ) {
+      moved = true;
+    }
+    if (--cseg_left == 0 && cseg < 2) {
+      if (cseg == 0) give();
+      enter(cseg, cseg, cu, cc, cseg_left, cstride);
+      if (split && cseg == 2 && cseg_left > 0) take(t3);
+      moved = true;
+    }
+    if constexpr (SQ) {
+      if (moved) {
         sq_cur = sq_next;
         if constexpr (!FOLDED) fast_unit = unit_fast();
       }
