@@ -645,6 +645,13 @@ __device__ __forceinline__ void stage_block(const MoeArgs &a, int row0, int rows
   const int nk = K / kKC;
   const int per_row = nk * 16;  // 16-byte pieces (8 values) per row
   const int total = rows * per_row;
+  // q / per_row as a multiply-high (exact: q < 2^16, per_row < 2^12)
+  const uint32_t magic = 0xFFFFFFFFu / static_cast<uint32_t>(per_row) + 1u;
+  // G1: x [T, H] (the host keeps its bytes below 2^31); G2: the block's
+  // gate / up rows [rows, 2I]
+  const __amdgpu_buffer_rsrc_t src_rsrc =
+      FIRST ? make_rsrc(a.x, a.T * a.H * 2)
+            : make_rsrc(a.act + static_cast<int64_t>(row0) * (2 * a.I), static_cast<int64_t>(rows) * (2 * a.I) * 2);
   constexpr int kBatch = FIRST ? 12 : 6;
   auto batch = [&](int q0, auto first_tag) __attribute__((always_inline)) {
     u32x4 v[kBatch];
@@ -656,16 +663,16 @@ __device__ __forceinline__ void stage_block(const MoeArgs &a, int row0, int rows
     for (int i = 0; i < kBatch; ++i) {
       const int q0i = q0 + i * kSThreads + static_cast<int>(threadIdx.x);
       const int q = q0i < total ? q0i : total - 1;
-      const int r = q / per_row;
+      const int r = static_cast<int>(__umulhi(static_cast<uint32_t>(q), magic));
       const int rem = q - r * per_row;
       const int c = rem >> 4, pc = rem & 15;
+      const int col = 2 * (c * kKC + pc * 8);  // byte offset within the row
       if constexpr (FIRST) {
-        const int64_t src = static_cast<int64_t>(rtok[r]) * a.H + c * kKC + pc * 8;
-        v[i] = *reinterpret_cast<const u32x4 *>(a.x + src);
+        v[i] = __builtin_amdgcn_raw_buffer_load_b128(src_rsrc, rtok[r] * (2 * a.H) + col, 0, 0);
       } else {
-        const int64_t src = static_cast<int64_t>(row0 + r) * (2 * a.I) + c * kKC + pc * 8;
-        v[i] = *reinterpret_cast<const u32x4 *>(a.act + src);           // gate, 8 features
-        vu[i] = *reinterpret_cast<const u32x4 *>(a.act + src + a.I);    // up, same features
+        const int off = r * (4 * a.I) + col;
+        v[i] = __builtin_amdgcn_raw_buffer_load_b128(src_rsrc, off, 0, 0);            // gate, 8 features
+        vu[i] = __builtin_amdgcn_raw_buffer_load_b128(src_rsrc, off + 2 * a.I, 0, 0);  // up, same features
       }
       dst[i] = q0i < total ? (c * kRowsMax + r) * kRowBytes + 16 * (pc ^ (r & 15)) : -1;
     }
@@ -875,19 +882,37 @@ __device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, 
 #pragma unroll
   for (int rt = 0; rt < NRT; ++rt) tot[rt][0] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
+  // epilogue targets of this lane's rows m = rt*16 + 4*lg + j (32-bit
+  // element offsets: the host bounds T*k*max(H, I)*4 below 2^31): G1 writes
+  // row row0 + m of the gate / up pre-activations, G2 the slot output of
+  // assignment rasg[m] scaled by its routing weight
+  const int ld = FIRST ? 2 * a.I : a.H;
+  int eoff[NRT][4];
+  float ewt[NRT][FIRST ? 1 : 4];
+#pragma unroll
+  for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = rt * 16 + 4 * lg + j;
+      if constexpr (FIRST) {
+        eoff[rt][j] = m < rows ? (row0 + m) * ld + lc : -1;
+      } else {
+        const int asg = m < rows ? rasg[m] : 0;
+        eoff[rt][j] = m < rows ? asg * ld + lc : -1;
+        ewt[rt][j] = m < rows ? a.topk_w[asg] : 0.0f;
+      }
+    }
   auto epilogue = [&](int u) __attribute__((always_inline)) {
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int m = rt * 16 + 4 * lg + j;
-        if (m < rows) {
+        if (eoff[rt][j] >= 0) {
           if constexpr (FIRST) {
-            // gate (u < I / 16) or up pre-activation, rounded to bf16
-            a.act[static_cast<int64_t>(row0 + m) * (2 * a.I) + 16 * u + lc] = f32_to_bf16_bits(tot[rt][0][j]);
+            // gate (u < I / 16) or up pre-activation, rounded to bf16 (RNE)
+            a.act[eoff[rt][j] + 16 * u] = static_cast<uint16_t>(cvt2(tot[rt][0][j], 0.0f));
           } else {
-            const int asg = rasg[m];
-            a.ybuf[static_cast<int64_t>(asg) * a.H + 16 * u + lc] = tot[rt][0][j] * a.topk_w[asg];
+            a.ybuf[eoff[rt][j] + 16 * u] = tot[rt][0][j] * ewt[rt][j];
           }
         }
       }
