@@ -634,13 +634,11 @@ constexpr size_t kStaticLds = 8192;
 // Token rows [row0, row0 + rows) of one block, whole K, into LDS chunk tiles.
 // G1 copies x into K-slot order; G2 builds act = SwiGLU(g, u) from
 // the gate / up pre-activations and permutes it into K-slot order.
-// issue_codes() runs right after the last batch of row loads is issued:
-// the load counter retires in order, so rows loaded before the first codes
-// are written to LDS without waiting for those codes.  A block of <= 32
-// rows with K <= 12 * 128 (G1) or 6 * 128 (G2) is one batch.
-template <bool FIRST, class IssueCodes>
+// A block of <= 32 rows with K <= 12 * 128 (G1) or 6 * 128 (G2) is one
+// batch of loads, all in flight at once.
+template <bool FIRST>
 __device__ __forceinline__ void stage_block(const MoeArgs &a, int row0, int rows, const int32_t *rtok,
-                                            unsigned char *lds, IssueCodes issue_codes) {
+                                            unsigned char *lds) {
   const int K = FIRST ? a.H : a.I;
   const int nk = K / kKC;
   const int per_row = nk * 16;  // 16-byte pieces (8 values) per row
@@ -653,7 +651,7 @@ __device__ __forceinline__ void stage_block(const MoeArgs &a, int row0, int rows
       FIRST ? make_rsrc(a.x, a.T * a.H * 2)
             : make_rsrc(a.act + static_cast<int64_t>(row0) * (2 * a.I), static_cast<int64_t>(rows) * (2 * a.I) * 2);
   constexpr int kBatch = FIRST ? 12 : 6;
-  auto batch = [&](int q0, auto first_tag) __attribute__((always_inline)) {
+  auto batch = [&](int q0) __attribute__((always_inline)) {
     u32x4 v[kBatch];
     u32x4 vu[FIRST ? 1 : kBatch];
     int dst[kBatch];
@@ -676,11 +674,6 @@ __device__ __forceinline__ void stage_block(const MoeArgs &a, int row0, int rows
       }
       dst[i] = q0i < total ? (c * kRowsMax + r) * kRowBytes + 16 * (pc ^ (r & 15)) : -1;
     }
-    if constexpr (decltype(first_tag)::value) {
-      __builtin_amdgcn_sched_barrier(0);
-      issue_codes();
-      __builtin_amdgcn_sched_barrier(0);
-    }
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) {
       u32x4 o = v[i];
@@ -702,11 +695,7 @@ __device__ __forceinline__ void stage_block(const MoeArgs &a, int row0, int rows
       if (dst[i] >= 0) *reinterpret_cast<u32x4 *>(lds + dst[i]) = o;
     }
   };
-  // earlier batches (large blocks only) first, so no row load is issued
-  // after the codes
-  const int nbatch = (total + kBatch * kSThreads - 1) / (kBatch * kSThreads);
-  for (int bi = 0; bi + 1 < nbatch; ++bi) batch(bi * kBatch * kSThreads, std::false_type{});
-  batch((nbatch - 1) * kBatch * kSThreads, std::true_type{});
+  for (int q0 = 0; q0 < total; q0 += kBatch * kSThreads) batch(q0);
 }
 
 // the steps of one run of KD chunks, unrolled (step(integral_constant<d>))
@@ -951,20 +940,24 @@ __device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, 
   // refills it with chunk d of the next run
   WChunk<BITS> wb[KD][1];
   float sb[KD][1];
-  // the block's token rows are staged while the first codes are in flight
+  // the block's token rows, then the first run of codes
   __syncthreads();  // the previous block's rows and hand-over slots are no longer read
   if (lane == 0) hand_flag[wave] = 0;
-  stage_block<FIRST>(a, row0, rows, rtok, lds, [&]() __attribute__((always_inline)) {
-    if constexpr (SQ) load_sq(sq_cur);
-    run_steps<KD>([&](auto d_tag) __attribute__((always_inline)) {
-      constexpr int d = decltype(d_tag)::value;
-      load_w(d_tag, wb[d], sb[d]);
-      __builtin_amdgcn_sched_barrier(0);
-    });
-    next_run();
-  });
+  stage_block<FIRST>(a, row0, rows, rtok, lds);
   __syncthreads();
   if (nruns == 0) return;
+  // The first run's codes go out after the barrier: at the kernel's start
+  // every CU asks for a run per wave at once, and a wave waits at the issue
+  // of its loads until the memory system takes them -- so each wave starts
+  // computing as soon as its own loads are out, instead of all waves
+  // waiting for the slowest one's.
+  if constexpr (SQ) load_sq(sq_cur);
+  run_steps<KD>([&](auto d_tag) __attribute__((always_inline)) {
+    constexpr int d = decltype(d_tag)::value;
+    load_w(d_tag, wb[d], sb[d]);
+    __builtin_amdgcn_sched_barrier(0);
+  });
+  next_run();
   // SQ: whether every scale of the current unit takes the fast dequant
   // (decided per unit, so a run is all fast or all exact-slow); scale slots
   // past the row's last group are not looked at
