@@ -3,27 +3,33 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c4|c3|c2|c1]
 
-A *step* is one quantized MoE layer over one batch: router (softmax top-k
-from logits, which also writes the K-slot permuted x), stable expert
-permutation and work list, persistent GEMM1 + SwiGLU, persistent GEMM2 +
-routed weight, top-k combine -- one ``lq_moe_layer`` call (five kernels on
-one stream).  Inputs are resident in HBM before the timed region; weights rotate
-over several independently quantized copies so every step streams its
-weights from HBM rather than from the 256 MB MALL.
+A *step* is one quantized MoE layer over one batch -- one ``lq_moe_layer``
+call on one stream: the router (softmax top-k from logits), the expert plan
+(stable permutation and row blocks; for T*k <= 2048 every GEMM workgroup
+derives its own block instead), the streaming GEMM1 (W1 gate and up tiles,
+bf16 pre-activations), the streaming GEMM2 (SwiGLU applied while staging,
+W2, routed weight) and the top-k combine.  Inputs are resident in HBM before
+the timed region; weights rotate over several independently quantized
+copies so every step streams its weights from HBM rather than from the
+256 MB MALL.
 
 Default workload (the north-star target): C4 of BASELINE.json -- 64 experts,
 hidden 2048, intermediate 1024, INT4 group 128 with MSE scales (grid 16),
 64 tokens ~N(0,1), top-8 routing with Zipf(1.1)-skewed router logits.
 
 One JSON line is printed.  Besides the contract fields it carries
-``roofline`` for the dominant kernel (GEMM1, the persistent W1 kernel with
-the SwiGLU epilogue: HBM-bound at C4/C2, MFMA-bound at C3), timed with HIP
-events recorded by the library on the kernel's own stream inside the timed
-region, per-stage times, the other weight form's timing
-(``folded_scales`` or ``exact_weights``), ``cpu_baseline`` (the reference's
-dequantize-then-matmul path on the host CPU, torch, bounded sample) and
-``gpu_dequant_then_gemm`` (the same layer as dequantize-to-BF16 with the HIP
-dequant kernel, then torch BF16 batched GEMMs on the same GPU).
+``roofline`` for the dominant kernel (GEMM1: HBM-bound at C4/C2,
+MFMA-bound at C3), timed with fence-free HIP events the library records on
+its own stream in a second pass over the same calls (the headline ``value``
+comes from a pass without markers); ``roofline.traffic`` is the HBM bytes
+per GEMM1 launch that ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE``
+measured for this configuration (the committed summary under profiles/,
+scaled by a device copy of known size), or null when no summary exists.
+Also per-stage times, the other weight form's timing (``folded_scales`` or
+``exact_weights``), ``cpu_baseline`` (the reference's dequantize-then-matmul
+path on the host CPU, torch, bounded sample) and ``gpu_dequant_then_gemm``
+(the same layer as dequantize-to-BF16 with the HIP dequant kernel, then
+torch BF16 batched GEMMs on the same GPU).
 """
 
 from __future__ import annotations
@@ -78,6 +84,26 @@ def copy_calibration(mib):
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"copy_calibration_bytes_per_launch": n, "launches": 5}), flush=True)
+
+
+def pmc_traffic(config, form, kernel="gemm1"):
+    """HBM bytes per launch of `kernel` from profiles/moe_gemm_<config>_pmc_traffic.txt, or None.
+
+    The summary holds lines ``traffic_bytes <kernel> <form> <bytes>``: FETCH_SIZE and WRITE_SIZE
+    per dispatch from two rocprofv3 --pmc runs of this bench, each scaled by what the counter
+    reads for a device copy of known size (the commands are in the file).
+    """
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        f"moe_gemm_{config}_pmc_traffic.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 4 and parts[0] == "traffic_bytes" and parts[1] == kernel and parts[2] == form:
+                    return int(parts[3])
+    except OSError:
+        return None
+    return None
 
 
 def zipf_logits(torch, T, E, seed, s=1.1):
@@ -288,8 +314,8 @@ def main():
     hip = Hip()
     hip.lib.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
     hip_stream = ctypes.c_void_p(stream.cuda_stream)
-    # stage boundaries of one lq_moe_layer call: 0 start, 1 route (+ x permute), 2 plan,
-    # 3 GEMM1 (+SwiGLU), 4 GEMM2 (+routed weight), 5 combine
+    # stage boundaries of one lq_moe_layer call: 0 start, 1 route, 2 plan (a marker only when
+    # the GEMMs plan their own blocks), 3 GEMM1, 4 GEMM2 (+SwiGLU, routed weight), 5 combine
     n_marks = 6
 
     def timed(calls, steps, warmup):
@@ -339,18 +365,19 @@ def main():
     n_active = int((torch.bincount(ids.reshape(-1).long(), minlength=E) > 0).sum())
     layer_b, g1_b, g2_b = layer_bytes(cfg, n_active)
     gemm1_ms = stage_ms[2]
-    kname = ("moe_stream_kernel<G1> (W1 gate and up tiles streamed per CU, in-kernel block plan)"
+    kname = ("moe_stream_kernel<G1> (W1 gate and up tiles streamed per CU)"
              if H % 512 == 0 and I % 512 == 0 else "moe_gemm_kernel<G1> (W1 gate+up, SwiGLU epilogue; persistent)")
+    traffic = pmc_traffic(args.config, "folded" if args.folded else "exact")
     if cfg["bound"] == "hbm":
         achieved = g1_b / (gemm1_ms / 1e3) / 1e9
         roofline = {"kernel": kname, "bound": "hbm", "achieved": round(achieved, 1), "peak": MI355X_HBM_GBPS,
-                    "unit": "GB/s", "frac": round(achieved / MI355X_HBM_GBPS, 4), "traffic": None,
+                    "unit": "GB/s", "frac": round(achieved / MI355X_HBM_GBPS, 4), "traffic": traffic,
                     "algorithmic_bytes": g1_b, "avg_ms": round(gemm1_ms, 5)}
     else:
         flops = 2.0 * T * k * 2 * I * H
         achieved = flops / (gemm1_ms / 1e3) / 1e12
         roofline = {"kernel": kname, "bound": "mfma", "achieved": round(achieved, 1), "peak": MI355X_BF16_TFLOPS,
-                    "unit": "TFLOP/s", "frac": round(achieved / MI355X_BF16_TFLOPS, 4), "traffic": None,
+                    "unit": "TFLOP/s", "frac": round(achieved / MI355X_BF16_TFLOPS, 4), "traffic": traffic,
                     "algorithmic_flops": flops, "avg_ms": round(gemm1_ms, 5)}
     stages = {name: round(v, 5) for name, v in zip(("route", "plan", "gemm1", "gemm2", "combine"), stage_ms)}
     stages["gemm2_gbps"] = round(g2_b / (stage_ms[3] / 1e3) / 1e9, 1)
