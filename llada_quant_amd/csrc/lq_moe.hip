@@ -1651,7 +1651,10 @@ int moe_forward_impl(const void *x, bool x_permuted, int64_t T, int H, int I, in
                                                                              xperm);
   }
   // small layers on the streaming GEMMs plan their blocks in-kernel
-  const bool inplan = stream && T * k <= kPlanMaxN;
+  // (every block of the in-kernel plan needs a CU of its own: there are at
+  // most ceil(T*k / 32) + min(E, T*k) blocks)
+  const int64_t nb_max = ceil_div(T * k, kRowsMax) + std::min<int64_t>(E, T * k);
+  const bool inplan = stream && T * k <= kPlanMaxN && nb_max <= device_info().cus;
   int rc = LQ_OK;
   if (!inplan) {
     plan_kernel<<<1, kPlanBlock, 0, st>>>(p);

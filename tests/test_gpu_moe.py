@@ -226,10 +226,26 @@ def test_streaming_one_hot_expert_many_blocks(dev):
     assert_close(out, oracle_out(x, q1, q2, ids, w))
 
 
+@pytest.mark.parametrize("E,T,k", [(128, 256, 8), (256, 256, 8), (64, 2, 8)])
+def test_streaming_many_experts(dev, E, T, k):
+    """Uniform routing over many experts at T*k <= 2048: E=128 keeps the GEMMs' own block
+    plan (up to 192 blocks, each needing a CU of its own); E=256 can produce more blocks
+    than a CU each can take, so the plan kernel runs instead.  T=2 leaves most CUs idle."""
+    H, I = 512, 512
+    q1, q2 = make_layer(dev, E, H, I, 4, seed=E + T)
+    g = torch.Generator().manual_seed(E)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    logits = torch.randn(T, E, generator=g).to(dev)
+    ids, w = route_topk(logits, k)
+    a = fused_moe_packed(x, q1, q2, ids, w)
+    assert torch.equal(a, fused_moe_packed(x, q1, q2, ids, w, general_kernel=True))
+    assert_close(a, oracle_out(x, q1, q2, ids, w))
+
+
 @pytest.mark.parametrize("T,k", [(64, 8), (600, 8)])
 def test_moe_layer_front_end_matches_router_then_forward(dev, T, k):
-    """moe_layer on a streaming shape: T*k <= 2048 takes the one-launch router + plan,
-    larger T the router kernel then the plan; both equal route_topk + fused_moe_packed."""
+    """moe_layer on a streaming shape: T*k <= 2048 lets the GEMMs plan their own
+    blocks, larger T runs the plan kernel; both equal route_topk + fused_moe_packed."""
     E, H, I = 32, 1024, 512
     q1, q2 = make_layer(dev, E, H, I, 4, seed=T)
     g = torch.Generator().manual_seed(T + 1)
