@@ -96,6 +96,8 @@ struct MoeArgs {
   const int32_t *srow;     // [T*k] token of each sorted row (sorted / k)
   const int4 *blocks;      // row blocks {expert, first sorted row, rows, 0}
   const PlanHeader *hdr;
+  int4 *slotplan;          // streaming, in-kernel plan: per CU slot {expert, first row, rows, i << 16 | m}
+  int32_t *slotasg;        // ... and the assignment of each of its block's rows [slot][kRowsMax]
   uint16_t *act;           // [T*k, I] bf16, by sorted row
   float *ybuf;             // [T*k, H] fp32, by assignment
   uint16_t *out;           // [T, H] bf16
@@ -1078,7 +1080,7 @@ __device__ __forceinline__ int xcd_slot(int g, int G) { return G % 8 ? g : (g % 
 // Slot c of G and its share of nb blocks: with nb <= G, slots
 // [ceil(b G / nb), ceil((b+1) G / nb)) share block b, slot c taking units
 // [i upb / m, (i+1) upb / m) of it; returns false for a slot without a block
-__device__ __forceinline__ bool cu_share(int c, int G, int nb, int upb, int &b, int &ub, int &ue) {
+__device__ __forceinline__ bool cu_share(int c, int G, int nb, int upb, int &b, int &ub, int &ue, int *im = nullptr) {
   b = static_cast<int>(static_cast<int64_t>(c) * nb / G);
   if (b >= nb) return false;
   const int first = static_cast<int>((static_cast<int64_t>(b) * G + nb - 1) / nb);
@@ -1086,6 +1088,7 @@ __device__ __forceinline__ bool cu_share(int c, int G, int nb, int upb, int &b, 
   const int m = next - first, i = c - first;
   ub = i * upb / m;
   ue = (i + 1) * upb / m;
+  if (im) *im = (i << 16) | m;
   return true;
 }
 
@@ -1102,7 +1105,7 @@ __device__ __forceinline__ bool cu_share(int c, int G, int nb, int upb, int &b, 
 // block.
 constexpr int kPlanMaxN = 2048;
 __device__ __forceinline__ bool block_plan(const MoeArgs &a, int upb, int &e, int &row0, int &rows, int &ub,
-                                           int &ue, int32_t *rtok, int32_t *rasg) {
+                                           int &ue, int &im, int32_t *rtok, int32_t *rasg) {
   __shared__ int cnt[kMaxExperts];
   __shared__ uint16_t ids_l[kPlanMaxN];  // expert of each assignment (0xFFFF: none)
   const int tid = threadIdx.x;
@@ -1150,7 +1153,7 @@ __device__ __forceinline__ bool block_plan(const MoeArgs &a, int upb, int &e, in
   }
   const int nb = __builtin_amdgcn_readlane(binc, 63);
   int b;
-  if (!cu_share(xcd_slot(blockIdx.x, gridDim.x), gridDim.x, nb, upb, b, ub, ue)) return false;
+  if (!cu_share(xcd_slot(blockIdx.x, gridDim.x), gridDim.x, nb, upb, b, ub, ue, &im)) return false;
   // the lane whose experts hold block b, then the expert within it
   const int bex = binc - bsum;
   const int owner = static_cast<int>(__builtin_ctzll(__ballot(bex <= b && b < binc)));
@@ -1200,15 +1203,39 @@ __device__ __forceinline__ bool block_plan(const MoeArgs &a, int upb, int &e, in
   return true;
 }
 
-template <int BITS, bool FOLDED, bool FIRST, int KD, bool SQ, bool INPLAN>
+// PLAN: kPlanTable -- the blocks come from plan_kernel's table;
+// kPlanOwn -- the workgroup plans its own block (block_plan) and records
+// it in slot records for the next GEMM; kPlanSlot -- the block comes from
+// the slot record the previous GEMM's workgroup of the same slot wrote
+// (same grid, same plan: one load instead of a plan).
+constexpr int kPlanTable = 0, kPlanOwn = 1, kPlanSlot = 2;
+
+template <int BITS, bool FOLDED, bool FIRST, int KD, bool SQ, int PLAN>
 __global__ __launch_bounds__(kSThreads, 1) void moe_stream_kernel(MoeArgs a) {
   extern __shared__ __align__(16) unsigned char slds[];
   const int upb = FIRST ? 2 * a.I / 16 : a.H / 16;  // units (16-row tiles) per row block
-  if constexpr (INPLAN) {
+  if constexpr (PLAN == kPlanOwn) {
     __shared__ int32_t rtok[kRowsMax], rasg[kRowsMax];
-    int e, row0, rows, ub, ue;
-    if (!block_plan(a, upb, e, row0, rows, ub, ue, rtok, rasg)) return;
+    const int slot = xcd_slot(blockIdx.x, gridDim.x);
+    int e, row0, rows, ub, ue, im;
+    if (!block_plan(a, upb, e, row0, rows, ub, ue, im, rtok, rasg)) {
+      if (threadIdx.x == 0) a.slotplan[slot] = make_int4(0, 0, 0, 0);
+      return;
+    }
+    if (threadIdx.x == 0) a.slotplan[slot] = make_int4(e, row0, rows, im);
+    if (static_cast<int>(threadIdx.x) < rows) a.slotasg[slot * kRowsMax + threadIdx.x] = rasg[threadIdx.x];
     stream_block<BITS, FOLDED, FIRST, KD, SQ>(a, e, row0, rows, rtok, rasg, ub, ue, slds);
+  } else if constexpr (PLAN == kPlanSlot) {
+    const int slot = xcd_slot(blockIdx.x, gridDim.x);
+    const int4 rec = a.slotplan[slot];
+    const int rows = __builtin_amdgcn_readfirstlane(rec.z);
+    if (rows == 0) return;
+    const int e = __builtin_amdgcn_readfirstlane(rec.x);
+    const int row0 = __builtin_amdgcn_readfirstlane(rec.y);
+    const int im = __builtin_amdgcn_readfirstlane(rec.w);
+    const int i = im >> 16, m = im & 0xFFFF;
+    stream_block<BITS, FOLDED, FIRST, KD, SQ>(a, e, row0, rows, nullptr, a.slotasg + slot * kRowsMax,
+                                              i * upb / m, (i + 1) * upb / m, slds);
   } else {
     const int nb = __builtin_amdgcn_readfirstlane(a.hdr->n_blk);
     const int G = gridDim.x, c = xcd_slot(blockIdx.x, gridDim.x);
@@ -1363,10 +1390,13 @@ __global__ __launch_bounds__(256) void permute_rows_kernel(const uint16_t *__res
 // ---------------------------------------------------------------------------
 
 struct WsLayout {
-  size_t counts, offsets, sorted, srow, hdr, blocks, ids, weights, xperm, act, ybuf, total;
+  size_t counts, offsets, sorted, srow, hdr, blocks, slotplan, slotasg, ids, weights, xperm, act, ybuf, total;
 };
 
 inline size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+// CU slots the streaming GEMMs' slot records cover (one workgroup per CU)
+constexpr int kMaxSlots = 1024;
 
 // row blocks of at most kRowsMax sorted rows: one partial block per expert at most
 int64_t max_blocks_for(int64_t T, int E, int k) {
@@ -1388,6 +1418,8 @@ WsLayout ws_layout(int64_t T, int H, int I, int E, int k) {
   take(w.srow, sizeof(int32_t) * N);
   take(w.hdr, sizeof(PlanHeader));
   take(w.blocks, sizeof(int4) * max_blocks_for(T, E, k));
+  take(w.slotplan, sizeof(int4) * kMaxSlots);
+  take(w.slotasg, sizeof(int32_t) * kMaxSlots * kRowsMax);
   take(w.ids, sizeof(int32_t) * N);
   take(w.weights, sizeof(float) * N);
   take(w.xperm, sizeof(uint16_t) * T * H);
@@ -1512,14 +1544,14 @@ bool stream_eligible(int bits, int H, int I, int64_t g1, int64_t g2) {
          lds + kStaticLds <= static_cast<size_t>(device_info().max_lds);
 }
 
-template <int BITS, bool FOLDED, bool FIRST, int KD, bool SQ, bool INPLAN>
+template <int BITS, bool FOLDED, bool FIRST, int KD, bool SQ, int PLAN>
 int launch_stream_kd(const MoeArgs &a, hipStream_t st) {
   const DeviceInfo dev = device_info();
   static std::once_flag attr_once;
   static hipError_t attr_rc = hipSuccess;
   std::call_once(attr_once, [&] {
     // dynamic LDS may take what the kernel's static LDS leaves
-    const void *fn = reinterpret_cast<const void *>(moe_stream_kernel<BITS, FOLDED, FIRST, KD, SQ, INPLAN>);
+    const void *fn = reinterpret_cast<const void *>(moe_stream_kernel<BITS, FOLDED, FIRST, KD, SQ, PLAN>);
     hipFuncAttributes fa{};
     attr_rc = hipFuncGetAttributes(&fa, fn);
     if (attr_rc == hipSuccess)
@@ -1529,14 +1561,16 @@ int launch_stream_kd(const MoeArgs &a, hipStream_t st) {
   if (attr_rc != hipSuccess)
     return fail(LQ_ERR_RUNTIME, std::string("hipFuncSetAttribute failed: ") + hipGetErrorString(attr_rc));
   const size_t lds = stream_lds_bytes(FIRST ? a.H : a.I);
-  moe_stream_kernel<BITS, FOLDED, FIRST, KD, SQ, INPLAN><<<dev.cus, kSThreads, lds, st>>>(a);
+  moe_stream_kernel<BITS, FOLDED, FIRST, KD, SQ, PLAN><<<dev.cus, kSThreads, lds, st>>>(a);
   return check_launch(FIRST ? "moe_stream_gemm1" : "moe_stream_gemm2");
 }
 
+// inplan: G1 plans its blocks in-kernel and records them per slot, G2
+// reads the records; otherwise both read plan_kernel's table
 template <int BITS, bool FOLDED, bool FIRST, int KD, bool SQ>
 int launch_stream_plan(const MoeArgs &a, hipStream_t st, bool inplan) {
-  return inplan ? launch_stream_kd<BITS, FOLDED, FIRST, KD, SQ, true>(a, st)
-                : launch_stream_kd<BITS, FOLDED, FIRST, KD, SQ, false>(a, st);
+  if (!inplan) return launch_stream_kd<BITS, FOLDED, FIRST, KD, SQ, kPlanTable>(a, st);
+  return launch_stream_kd<BITS, FOLDED, FIRST, KD, SQ, FIRST ? kPlanOwn : kPlanSlot>(a, st);
 }
 
 // chunks in flight per wave: 8 KB of codes where K allows (INT4: 8 x 1 KB,
@@ -1654,7 +1688,8 @@ int moe_forward_impl(const void *x, bool x_permuted, int64_t T, int H, int I, in
   // (every block of the in-kernel plan needs a CU of its own: there are at
   // most ceil(T*k / 32) + min(E, T*k) blocks)
   const int64_t nb_max = ceil_div(T * k, kRowsMax) + std::min<int64_t>(E, T * k);
-  const bool inplan = stream && T * k <= kPlanMaxN && nb_max <= device_info().cus;
+  const bool inplan =
+      stream && T * k <= kPlanMaxN && nb_max <= device_info().cus && device_info().cus <= kMaxSlots;
   int rc = LQ_OK;
   if (!inplan) {
     plan_kernel<<<1, kPlanBlock, 0, st>>>(p);
@@ -1677,6 +1712,8 @@ int moe_forward_impl(const void *x, bool x_permuted, int64_t T, int H, int I, in
   a.blocks = p.blocks;
   a.srow = p.srow;
   a.hdr = p.hdr;
+  a.slotplan = reinterpret_cast<int4 *>(ws + w.slotplan);
+  a.slotasg = reinterpret_cast<int32_t *>(ws + w.slotasg);
   a.act = reinterpret_cast<uint16_t *>(ws + w.act);
   a.ybuf = reinterpret_cast<float *>(ws + w.ybuf);
   a.out = static_cast<uint16_t *>(out);
