@@ -1080,11 +1080,14 @@ __device__ __forceinline__ int xcd_slot(int g, int G) { return G % 8 ? g : (g % 
 // Slot c of G and its share of nb blocks: with nb <= G, slots
 // [ceil(b G / nb), ceil((b+1) G / nb)) share block b, slot c taking units
 // [i upb / m, (i+1) upb / m) of it; returns false for a slot without a block
+// (Wide: 64-bit products, for plan_kernel's tables of any size; the
+// in-kernel plan has nb <= G <= 1024 and takes 32-bit arithmetic.)
+template <typename Wide = int64_t>
 __device__ __forceinline__ bool cu_share(int c, int G, int nb, int upb, int &b, int &ub, int &ue, int *im = nullptr) {
-  b = static_cast<int>(static_cast<int64_t>(c) * nb / G);
+  b = static_cast<int>(static_cast<Wide>(c) * nb / G);
   if (b >= nb) return false;
-  const int first = static_cast<int>((static_cast<int64_t>(b) * G + nb - 1) / nb);
-  const int next = static_cast<int>((static_cast<int64_t>(b + 1) * G + nb - 1) / nb);
+  const int first = static_cast<int>((static_cast<Wide>(b) * G + nb - 1) / nb);
+  const int next = static_cast<int>((static_cast<Wide>(b + 1) * G + nb - 1) / nb);
   const int m = next - first, i = c - first;
   ub = i * upb / m;
   ue = (i + 1) * upb / m;
@@ -1153,7 +1156,7 @@ __device__ __forceinline__ bool block_plan(const MoeArgs &a, int upb, int &e, in
   }
   const int nb = __builtin_amdgcn_readlane(binc, 63);
   int b;
-  if (!cu_share(xcd_slot(blockIdx.x, gridDim.x), gridDim.x, nb, upb, b, ub, ue, &im)) return false;
+  if (!cu_share<uint32_t>(xcd_slot(blockIdx.x, gridDim.x), gridDim.x, nb, upb, b, ub, ue, &im)) return false;
   // the lane whose experts hold block b, then the expert within it
   const int bex = binc - bsum;
   const int owner = static_cast<int>(__builtin_ctzll(__ballot(bex <= b && b < binc)));
@@ -1179,6 +1182,8 @@ __device__ __forceinline__ bool block_plan(const MoeArgs &a, int upb, int &e, in
   // stable compaction of expert e's assignments, keeping ranks [first, first + rows)
   const unsigned long long lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
   const int last = first + rows;
+  // i / k by multiply-high (exact for i < 2^16; k == 1 would need 2^32)
+  const uint32_t kmagic = a.k > 1 ? 0xFFFFFFFFu / static_cast<uint32_t>(a.k) + 1u : 0u;
   int run = 0;
   for (int c0 = 0; c0 < N && run < last; c0 += 256) {
     int idv[4];
@@ -1195,7 +1200,7 @@ __device__ __forceinline__ bool block_plan(const MoeArgs &a, int upb, int &e, in
       const int rank = run + __popcll(bal & lt);
       if (hit && rank >= first && rank < last) {
         rasg[rank - first] = i;
-        rtok[rank - first] = i / a.k;
+        rtok[rank - first] = a.k > 1 ? static_cast<int>(__umulhi(static_cast<uint32_t>(i), kmagic)) : i;
       }
       run += __popcll(bal);
     }
