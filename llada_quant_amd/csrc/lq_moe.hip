@@ -582,6 +582,19 @@ __global__ __launch_bounds__(kThreads, 3) void moe_gemm_kernel(MoeArgs a) {
   }
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave with DPP lane moves:
+// row_shr 1, 2, 4, 8 within each row of 16 lanes (lanes without a source
+// add 0), then row_bcast 15 and 31 carry the row totals into later rows.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15 into rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31 into rows 2, 3
+  return v;
+}
+
 // exclusive scan of in[0..E) by wave 0 (lane l owns entries 4l..4l+3)
 __device__ void wave0_exclusive_scan(const int *in, int *out, int E, int *total) {
   const int lane = threadIdx.x & 63;
@@ -1144,16 +1157,7 @@ __device__ __forceinline__ bool block_plan(const MoeArgs &a, int upb, int &e, in
     csum += c[i];
     bsum += nbk[i];
   }
-  int cinc = csum, binc = bsum;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int yc = __shfl_up(cinc, o, 64);
-    const int yb = __shfl_up(binc, o, 64);
-    if (lane >= o) {
-      cinc += yc;
-      binc += yb;
-    }
-  }
+  const int cinc = wave_incl_scan(csum), binc = wave_incl_scan(bsum);
   const int nb = __builtin_amdgcn_readlane(binc, 63);
   int b;
   if (!cu_share<uint32_t>(xcd_slot(blockIdx.x, gridDim.x), gridDim.x, nb, upb, b, ub, ue, &im)) return false;
