@@ -1304,9 +1304,17 @@ __device__ __forceinline__ void plan_body(const PlanArgs &p, IdAt id_at) {
   for (int e = tid; e < kMaxExperts; e += kPlanBlock) hist[e] = 0;
   for (int i = tid; i < kPlanWaves * kMaxExperts; i += kPlanBlock) (&wcnt[0][0])[i] = 0;
   __syncthreads();
-  for (int64_t a = tid; a < p.N; a += kPlanBlock) {
-    const int id = id_at(a);
-    if (id >= 0 && id < E) atomicAdd(&hist[id], 1);
+  // (8 ids per thread in flight at once: the loop is latency-bound otherwise)
+  for (int64_t a0 = 0; a0 < p.N; a0 += 8 * kPlanBlock) {
+    int idv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t a = a0 + j * kPlanBlock + tid;
+      idv[j] = a < p.N ? id_at(a) : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (idv[j] >= 0 && idv[j] < E) atomicAdd(&hist[idv[j]], 1);
   }
   __syncthreads();
   if (wave == 0) wave0_exclusive_scan(hist, base, E, &total);
@@ -1349,9 +1357,12 @@ __device__ __forceinline__ void plan_body(const PlanArgs &p, IdAt id_at) {
   int nbits = 1;
   while ((1 << nbits) <= E) ++nbits;
   const unsigned long long lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  // the next chunk's id is loaded while this chunk is ranked and scattered
+  int next = tid < p.N ? id_at(tid) : -1;
   for (int64_t chunk = 0; chunk < p.N; chunk += kPlanBlock) {
     const int64_t a = chunk + tid;
-    const int raw = a < p.N ? id_at(a) : -1;
+    const int raw = next;
+    next = a + kPlanBlock < p.N ? id_at(a + kPlanBlock) : -1;
     const bool valid = raw >= 0 && raw < E;
     const int key = valid ? raw : E;
     unsigned long long peers = ~0ull;
