@@ -64,6 +64,8 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-gpu-baseline", action="store_true", help="skip the dequantize-then-GEMM leg")
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--kernel", choices=("auto", "stream", "general", "wide"), default="auto",
+                   help="GEMM family (auto: the library's own choice for the shape)")
     p.add_argument("--folded", action="store_true",
                    help="time the LQ_MOE_FOLDED_SCALES form (integer codes, fp32 group scale) as the headline")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -104,6 +106,24 @@ def pmc_traffic(config, form, kernel="gemm1"):
     except OSError:
         return None
     return None
+
+
+KERNEL_NAMES = {
+    "wide": "moe_wide_kernel<G1> (blocks of <= 128 rows, 4 weight tiles x 8 row tiles per wave, SwiGLU epilogue)",
+    "stream": "moe_stream_kernel<G1> (W1 gate and up tiles streamed per CU)",
+    "general": "moe_gemm_kernel<G1> (W1 gate+up, SwiGLU epilogue; persistent)",
+}
+
+
+def kernel_family(cfg, folded, forced):
+    """The GEMM family lq_moe_layer runs for this shape (the library's rule), or the forced one."""
+    if forced != "auto":
+        return forced
+    E, H, I, k, T = cfg["experts"], cfg["hidden"], cfg["inter"], cfg["top_k"], cfg["tokens"]
+    if not folded and H % 256 == 0 and I % 128 == 0 and T * k >= 128 * E:
+        return "wide"
+    step = 512 if cfg["bits"] == 4 else 256
+    return "stream" if H % step == 0 and I % step == 0 else "general"
 
 
 def zipf_logits(torch, T, E, seed, s=1.1):
@@ -356,7 +376,9 @@ def main():
                 hip.destroy(m)
         return stage_ms
 
-    calls = make_calls(_lib.LQ_MOE_FOLDED_SCALES if args.folded else 0)
+    family = kernel_family(cfg, args.folded, args.kernel)
+    kflag = {"wide": _lib.LQ_MOE_WIDE_KERNEL, "general": _lib.LQ_MOE_GENERAL_KERNEL}.get(args.kernel, 0)
+    calls = make_calls((_lib.LQ_MOE_FOLDED_SCALES if args.folded else 0) | kflag)
     wall0 = time.perf_counter()
     ms_per_step = timed(calls, args.steps, args.warmup)
     wall = time.perf_counter() - wall0
@@ -365,8 +387,7 @@ def main():
     n_active = int((torch.bincount(ids.reshape(-1).long(), minlength=E) > 0).sum())
     layer_b, g1_b, g2_b = layer_bytes(cfg, n_active)
     gemm1_ms = stage_ms[2]
-    kname = ("moe_stream_kernel<G1> (W1 gate and up tiles streamed per CU)"
-             if H % 512 == 0 and I % 512 == 0 else "moe_gemm_kernel<G1> (W1 gate+up, SwiGLU epilogue; persistent)")
+    kname = KERNEL_NAMES[family]
     traffic = pmc_traffic(args.config, "folded" if args.folded else "exact")
     if cfg["bound"] == "hbm":
         achieved = g1_b / (gemm1_ms / 1e3) / 1e9
@@ -381,7 +402,9 @@ def main():
                     "algorithmic_flops": flops, "avg_ms": round(gemm1_ms, 5)}
     stages = {name: round(v, 5) for name, v in zip(("route", "plan", "gemm1", "gemm2", "combine"), stage_ms)}
     stages["gemm2_gbps"] = round(g2_b / (stage_ms[3] / 1e3) / 1e9, 1)
-    other_calls = make_calls(0 if args.folded else _lib.LQ_MOE_FOLDED_SCALES)
+    # the other weight form (the wide kernels take exact weights only)
+    other_calls = make_calls(0 | kflag if args.folded else
+                             _lib.LQ_MOE_FOLDED_SCALES | (kflag if args.kernel == "general" else 0))
     other_ms = timed(other_calls, max(10, args.steps // 4), 3)
     other_stage = staged(other_calls, max(10, args.steps // 4))
 
@@ -405,6 +428,7 @@ def main():
             "experts": E, "hidden": H, "intermediate": I, "top_k": k, "tokens": T, "bits": cfg["bits"],
             "group_size": 128, "active_experts": n_active, "weight_copies": copies,
             "weights_in_mfma": "folded: exact codes, fp32 group scale" if args.folded else "exact bf16(fp32(q)*s)",
+            "gemm_family": family,
             "layer_algorithmic_bytes": layer_b,
             "layer_gbps": round(layer_b / (ms_per_step / 1e3) / 1e9, 1),
             "wall_ms_per_step": round(wall / (args.steps + args.warmup) * 1e3, 5),

@@ -582,6 +582,303 @@ __global__ __launch_bounds__(kThreads, 3) void moe_gemm_kernel(MoeArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// wide G1 / G2 kernels (the matrix-core regime: hundreds of rows per expert)
+//
+// An item is (row block of up to 128 sorted rows of one expert, slice of
+// weight rows).  Four waves, one per SIMD, so each holds 512 registers (its
+// 128 accumulators in AGPRs); wave w owns four 16-row weight tiles over the
+// whole K -- G1: the gate and up rows of features [32w, 32w + 32) of the
+// slice (128 features per item), so SwiGLU stays lane-local; G2: output
+// rows [64w, 64w + 64) of the slice (256 per item) -- and multiplies each
+// dequantized B fragment with up to 8 row tiles staged in LDS.  One
+// dequantization then feeds 128 rows instead of 32, which keeps the weight
+// arithmetic (~18 VALU per 8 weights, 4 cycles each) below the matrix-core
+// time of the fragment (8 x v_mfma_f32_16x16x32_bf16, 16 cycles each), and
+// each A fragment read from LDS feeds four MFMAs.
+// Token rows are staged one 128-wide K chunk at a time by all 256 threads
+// (double buffered, 32 KB per stage, one barrier per chunk), one chunk
+// ahead; weight codes are loaded two chunks ahead into registers.  The
+// per-chunk arithmetic and its order are chunk_mfma's (wide_chunk), as in
+// the other GEMM families, so all of them agree bit for bit.
+// Items are cut into 8 contiguous ranges, one per XCD, block-major: the
+// slices of one block (the same token rows) and the blocks of one expert
+// (the same weights) run at about the same time on one L2.
+// ---------------------------------------------------------------------------
+constexpr int kWWaves = 4;
+constexpr int kWThreads = 64 * kWWaves;
+constexpr int kWRows = 128;                  // sorted rows per wide row block
+constexpr int kWF1 = kWWaves * 32;           // G1 features per item
+constexpr int kWR2 = kWWaves * 64;           // G2 output rows per item
+constexpr int kWStage = kWRows * kRowBytes;  // one LDS stage: 128 rows x 128 K bf16
+
+// One 128-wide K chunk of the wide kernels: chunk_mfma's arithmetic in
+// chunk_mfma's order, software-pipelined for one wave per SIMD.  The four
+// 32-wide K steps s run with the A fragments of step s + 1 read from LDS
+// and the B fragments of step s + 1 dequantized while the MFMAs of step s
+// execute (two register sets, ping-pong), so neither the LDS latency nor the
+// weight arithmetic stalls the matrix core; sched_group_barrier interleaves
+// one MFMA with a share of the reads and VALU work.
+template <int BITS, bool FAST, int NRT, int NT>
+__device__ __forceinline__ void wide_chunk(const WChunk<BITS> (&w)[NT], const float (&sc)[NT],
+                                           const unsigned char *buf, int lc, int lg, floatx4 (&tot)[NRT][NT]) {
+  DqScale dqs[NT];
+#pragma unroll
+  for (int c = 0; c < NT; ++c) dqs[c] = dq_scale<BITS>(sc[c]);
+  auto bfrag = [&](int s, uint4(&b)[NT]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int c = 0; c < NT; ++c) {
+      if constexpr (BITS == 4) {
+        const uint32_t q = s == 0 ? w[c].v.x : s == 1 ? w[c].v.y : s == 2 ? w[c].v.z : w[c].v.w;
+        b[c] = b_int4_exact<FAST>(q, sc[c], dqs[c]);
+      } else {
+        const uint4 &v = s < 2 ? w[c].v0 : w[c].v1;
+        b[c] = b_int8_exact<FAST>((s & 1) ? v.z : v.x, (s & 1) ? v.w : v.y, sc[c], dqs[c]);
+      }
+    }
+  };
+  auto afrag = [&](int s, uint4(&a)[NRT]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+      a[rt] = *reinterpret_cast<const uint4 *>(buf + (rt * 16 + lc) * kRowBytes + 16 * ((4 * lg + s) ^ lc));
+  };
+  // VALU instructions to place after each MFMA (the dequant of one step is
+  // ~18 per tile)
+  constexpr int kValuPer = (18 * NT + NRT * NT - 1) / (NRT * NT);
+  auto step = [&](int s, const uint4(&ac)[NRT], const uint4(&bc)[NT], uint4(&an)[NRT], uint4(&bn)[NT])
+                  __attribute__((always_inline)) {
+    if (s < 3) {
+      afrag(s + 1, an);
+      bfrag(s + 1, bn);
+    }
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+      for (int c = 0; c < NT; ++c)
+        tot[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ac[rt]), as_bf16x8(bc[c]), tot[rt][c], 0, 0, 0);
+    if (s < 3) {
+#pragma unroll
+      for (int rt = 0; rt < NRT; ++rt) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+        __builtin_amdgcn_sched_group_barrier(0x002, kValuPer, 0);
+#pragma unroll
+        for (int c = 1; c < NT; ++c) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, kValuPer, 0);
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  uint4 a0[NRT], a1[NRT], b0[NT], b1[NT];
+  afrag(0, a0);
+  bfrag(0, b0);
+  step(0, a0, b0, a1, b1);
+  step(1, a1, b1, a0, b0);
+  step(2, a0, b0, a1, b1);
+  step(3, a1, b1, a0, b0);
+}
+
+template <int BITS, int NRT, bool FIRST, bool G128>
+__device__ __forceinline__ void wide_item(const MoeArgs &a, int e, int slice, int row0, int rows,
+                                          unsigned char *lds) {
+  static_assert(NRT == 2 || NRT == 4 || NRT == 8, "row tiles per block");
+  constexpr int NQ = NRT * 256 / kWThreads;  // staged pieces per thread and chunk: NRT * 16 rows x 16 pieces
+  constexpr int NT = 4;        // weight tiles per wave
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int lc = lane & 15;
+  const int lg = lane >> 4;
+  const int K = FIRST ? a.H : a.I;
+  const int nk = K / kKC;  // K is a multiple of 128 on this path (host-checked)
+
+  // ---- token rows: piece tid + 256 q of a chunk is row r = piece >> 4,
+  // 16-byte piece lc of the row's 128 K values, stored at slot lc ^ (r & 15)
+  // (the XOR swizzle chunk_mfma reads).  Rows arrive K-slot permuted (xperm,
+  // act); rows past the block re-read its first row and are never stored out.
+  const __amdgpu_buffer_rsrc_t arsrc = make_rsrc(FIRST ? static_cast<const void *>(a.xperm) : a.act,
+                                                 FIRST ? a.T * a.H * 2 : a.T * a.k * a.I * 2);
+  const __amdgpu_buffer_rsrc_t empty = make_rsrc(a.out, 0);
+  int avoff[NQ], ldsoff[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int r = (tid + kWThreads * q) >> 4;
+    const int rr = r < rows ? r : 0;
+    const int rowelem = FIRST ? a.srow[row0 + rr] * a.H : (row0 + rr) * a.I;
+    avoff[q] = 2 * (rowelem + 8 * lc);
+    ldsoff[q] = r * kRowBytes + 16 * (lc ^ (r & 15));
+  }
+  auto load_a = [&](int i, u32x4(&v)[NQ]) __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t r = i < nk ? arsrc : empty;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) v[q] = __builtin_amdgcn_raw_buffer_load_b128(r, avoff[q], i * kKC * 2, 0);
+  };
+  auto store_a = [&](int i, const u32x4(&v)[NQ]) __attribute__((always_inline)) {
+    unsigned char *buf = lds + (i & 1) * kWStage;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) *reinterpret_cast<u32x4 *>(buf + ldsoff[q]) = v[q];
+  };
+
+  // ---- weights: tiles c = 0, 1 are gate rows of features 16c + lc of the
+  // wave's 32 (G1), c = 2, 3 the up rows of the same features; G2: output
+  // rows 16c + lc of the wave's 64
+  const int rowbytes = BITS == 4 ? (K >> 1) : K;
+  const int G = FIRST ? a.g1 : a.g2;
+  const int ng = FIRST ? a.ng1 : a.ng2;
+  const int nrows_w = FIRST ? 2 * a.I : a.H;
+  const __amdgpu_buffer_rsrc_t wrsrc =
+      make_rsrc((FIRST ? a.q1 : a.q2) + static_cast<int64_t>(e) * nrows_w * rowbytes,
+                static_cast<int64_t>(nrows_w) * rowbytes);
+  const __amdgpu_buffer_rsrc_t srsrc = make_rsrc((FIRST ? a.s1 : a.s2) + static_cast<int64_t>(e) * nrows_w * ng,
+                                                 static_cast<int64_t>(nrows_w) * ng * 4);
+  constexpr int kLaneBytes = BITS == 4 ? 16 : 32;  // one lane's 32 codes of a chunk
+  constexpr int kChunkBytes = BITS == 4 ? 64 : 128;
+  const int fbase = slice * kWF1 + 32 * wave;  // G1: the wave's first feature
+  const int obase = slice * kWR2 + 64 * wave;  // G2: the wave's first output row
+  int wvoff[NT], svoff[NT];
+#pragma unroll
+  for (int c = 0; c < NT; ++c) {
+    const int wr = FIRST ? (c < 2 ? 0 : a.I) + fbase + 16 * (c & 1) + lc : obase + 16 * c + lc;
+    wvoff[c] = wr * rowbytes + kLaneBytes * lg;
+    svoff[c] = wr * ng * 4;
+  }
+  auto load_w = [&](int i, WChunk<BITS>(&w)[NT], float(&sc)[NT]) __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t rw = i < nk ? wrsrc : empty;
+    const __amdgpu_buffer_rsrc_t rs = i < nk ? srsrc : empty;
+#pragma unroll
+    for (int c = 0; c < NT; ++c) {
+      if constexpr (BITS == 4) {
+        w[c].v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, wvoff[c], i * kChunkBytes, 0));
+      } else {
+        w[c].v0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, wvoff[c], i * kChunkBytes, 0));
+        w[c].v1 =
+            __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, wvoff[c] + 16, i * kChunkBytes, 0));
+      }
+      if constexpr (G128) {
+        sc[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, svoff[c], i * 4, 0));
+      } else {
+        const int sidx = (i * kKC + 32 * lg) / G;  // group of this lane's 32 K values
+        sc[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, svoff[c] + 4 * sidx, 0, 0));
+      }
+    }
+  };
+
+  floatx4 tot[NRT][NT];
+#pragma unroll
+  for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+    for (int c = 0; c < NT; ++c) tot[rt][c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  auto compute = [&](int i, const WChunk<BITS>(&w)[NT], const float(&sc)[NT]) __attribute__((always_inline)) {
+    const unsigned char *buf = lds + (i & 1) * kWStage;
+    if (__all(dq_fast_ok(sc[0]) && dq_fast_ok(sc[1]) && dq_fast_ok(sc[2]) && dq_fast_ok(sc[3])))
+      wide_chunk<BITS, true, NRT, NT>(w, sc, buf, lc, lg, tot);
+    else
+      wide_chunk<BITS, false, NRT, NT>(w, sc, buf, lc, lg, tot);
+  };
+
+  // Schedule (loads of a wave complete in issue order):
+  //   prologue: tokens 0 -> LDS stage 0, weights 0; tokens 1 -> registers, weights 1
+  //   step i:   compute chunk i (weights slot i & 1, LDS stage i & 1);
+  //             tokens i+1: registers -> LDS stage (i+1) & 1 (waits for them only:
+  //             weights i+1 were issued after them); issue tokens i+2 and
+  //             weights i+2 (into slot i & 1); barrier.
+  // Steps past the last chunk compute nothing and load out of range.
+  WChunk<BITS> wb[2][NT];
+  float sb[2][NT];
+  u32x4 av[NQ];
+  load_a(0, av);
+  __builtin_amdgcn_sched_barrier(0);
+  load_w(0, wb[0], sb[0]);
+  __builtin_amdgcn_sched_barrier(0);
+  store_a(0, av);
+  load_a(1, av);
+  __builtin_amdgcn_sched_barrier(0);
+  load_w(1, wb[1], sb[1]);
+  __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();  // chunk 0 staged
+  auto step = [&](int i, auto d_tag) __attribute__((always_inline)) {
+    constexpr int d = decltype(d_tag)::value;
+    if (i < nk) compute(i, wb[d], sb[d]);
+    __builtin_amdgcn_sched_barrier(0);
+    store_a(i + 1, av);
+    load_a(i + 2, av);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(i + 2, wb[d], sb[d]);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();  // chunk i consumed by every wave, chunk i + 1 staged
+  };
+  for (int i0 = 0; i0 < nk; i0 += 2) {
+    step(i0, std::integral_constant<int, 0>{});
+    step(i0 + 1, std::integral_constant<int, 1>{});
+  }
+
+  if constexpr (FIRST) {
+    // reference op order (INFERENCE_REPO_CHANGES.md:296-309): g, u -> bf16;
+    // silu in fp32 -> bf16; bf16 product; act stored K-slot permuted
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int f = kslot(fbase + 16 * c + lc);
+#pragma unroll
+      for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int m = rt * 16 + 4 * lg + j;
+          if (m < rows) {
+            const float gb = bf16_round(tot[rt][c][j]);
+            const float ub = bf16_round(tot[rt][c + 2][j]);
+            a.act[static_cast<int64_t>(row0 + m) * a.I + f] = static_cast<uint16_t>(swiglu_pk(gb, 0.0f, ub, 0.0f));
+          }
+        }
+    }
+  } else {
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int m = rt * 16 + 4 * lg + j;
+        if (m < rows) {
+          const int asg = a.sorted[row0 + m];
+          const float wt = a.topk_w[asg];
+          float *yrow = a.ybuf + static_cast<int64_t>(asg) * a.H + obase + lc;
+#pragma unroll
+          for (int c = 0; c < NT; ++c) yrow[16 * c] = tot[rt][c][j] * wt;
+        }
+      }
+  }
+}
+
+// Persistent wide G1 (FIRST) or G2 kernel over (row block, slice) items,
+// block-major, 8 contiguous ranges (one per XCD; workgroup g runs on XCD
+// g % 8, the grid is a multiple of 8), taken round-robin by the XCD's
+// workgroups.
+template <int BITS, bool FIRST, bool G128>
+__global__ __launch_bounds__(kWThreads, 1) void moe_wide_kernel(MoeArgs a) {
+  __shared__ __align__(16) unsigned char lds[2 * kWStage];
+  const int nb = __builtin_amdgcn_readfirstlane(a.hdr->n_blk);
+  const int per = FIRST ? a.I / kWF1 : a.H / kWR2;
+  const int n = nb * per;
+  const int xcd = blockIdx.x & 7;
+  const int gx = gridDim.x >> 3;
+  const int n8 = (n + 7) >> 3;
+  const int end = min(n, (xcd + 1) * n8);
+  for (int t = xcd * n8 + static_cast<int>(blockIdx.x >> 3); t < end; t += gx) {
+    const int blk = t / per;
+    const int slice = t - blk * per;
+    const int4 bi = a.blocks[blk];
+    const int e = __builtin_amdgcn_readfirstlane(bi.x);
+    const int row0 = __builtin_amdgcn_readfirstlane(bi.y);
+    const int rows = __builtin_amdgcn_readfirstlane(bi.z);
+    if (rows <= 32)
+      wide_item<BITS, 2, FIRST, G128>(a, e, slice, row0, rows, lds);
+    else if (rows <= 64)
+      wide_item<BITS, 4, FIRST, G128>(a, e, slice, row0, rows, lds);
+    else
+      wide_item<BITS, 8, FIRST, G128>(a, e, slice, row0, rows, lds);
+  }
+}
+
 // Inclusive prefix sum over the 64 lanes of a wave with DPP lane moves:
 // row_shr 1, 2, 4, 8 within each row of 16 lanes (lanes without a source
 // add 0), then row_bcast 15 and 31 carry the row totals into later rows.
@@ -1283,8 +1580,10 @@ struct PlanArgs {
   int32_t *sorted;
   int32_t *srow;  // token of each sorted row (nullptr: not written)
   int k;
-  // block table (blocks == nullptr: permutation only)
+  // block table (blocks == nullptr: permutation only) of blocks of at most
+  // block_rows sorted rows
   int4 *blocks;
+  int block_rows;
   PlanHeader *hdr;
 };
 
@@ -1327,12 +1626,13 @@ __device__ __forceinline__ void plan_body(const PlanArgs &p, IdAt id_at) {
 
   if (p.blocks != nullptr) {
     // row blocks per expert and their scan
-    for (int e = tid; e < E; e += kPlanBlock) wcnt[0][e] = (hist[e] + kRowsMax - 1) / kRowsMax;
+    const int br = p.block_rows;
+    for (int e = tid; e < E; e += kPlanBlock) wcnt[0][e] = (hist[e] + br - 1) / br;
     __syncthreads();
     if (wave == 0) wave0_exclusive_scan(wcnt[0], nbs, E, &nbs[E]);
     __syncthreads();
     // block table, expert-major: block b of expert e covers sorted rows
-    // [offsets[e] + 32 j, +32) with j = b - nbs[e]
+    // [offsets[e] + br j, + br) with j = b - nbs[e]
     const int nb_total = nbs[E];
     for (int b = tid; b < nb_total; b += kPlanBlock) {
       int lo = 0, hi = E;  // largest e with nbs[e] <= b
@@ -1342,8 +1642,8 @@ __device__ __forceinline__ void plan_body(const PlanArgs &p, IdAt id_at) {
         else hi = mid;
       }
       const int e = lo;
-      const int r0 = base[e] + (b - nbs[e]) * kRowsMax;
-      p.blocks[b] = make_int4(e, r0, min(kRowsMax, base[e] + hist[e] - r0), 0);
+      const int r0 = base[e] + (b - nbs[e]) * br;
+      p.blocks[b] = make_int4(e, r0, min(br, base[e] + hist[e] - r0), 0);
     }
     if (tid == 0) p.hdr->n_blk = nb_total;
     __syncthreads();
@@ -1492,6 +1792,18 @@ struct ProfileMarks {
   }
 };
 
+// The GEMM family a layer runs on.  Wide: many rows per expert (on average
+// at least kWideMinRows), where the matrix cores bound the layer; streaming:
+// the weight-bandwidth regime; general: every other supported shape.
+enum class Path { kStream, kGeneral, kWide };
+constexpr int kWideMinRows = 128;
+
+// the wide kernels need whole items along N (128 features, 256 output rows)
+// and exact weights (the folded form keeps its own kernels)
+bool wide_eligible(int H, int I, int flags) {
+  return H % kWR2 == 0 && I % kWF1 == 0 && !(flags & LQ_MOE_FOLDED_SCALES);
+}
+
 int validate_layer(const void *x, int64_t T, int H, int I, int E, int k, const int8_t *q1, const float *s1,
                    const int8_t *q2, const float *s2, int bits, int64_t group_w1, int64_t group_w2, int flags,
                    void *workspace, size_t ws_bytes, void *out) {
@@ -1500,7 +1812,14 @@ int validate_layer(const void *x, int64_t T, int H, int I, int E, int k, const i
   if (E < 1 || E > kMaxExperts)
     return fail(LQ_ERR_UNSUPPORTED, "moe_forward: 1 <= num_experts <= " + std::to_string(kMaxExperts));
   if (k > E) return fail(LQ_ERR_VALUE, "moe_forward: top_k exceeds num_experts");
-  if (flags & ~(LQ_MOE_FOLDED_SCALES | LQ_MOE_GENERAL_KERNEL)) return fail(LQ_ERR_VALUE, "moe_forward: unknown flags");
+  if (flags & ~(LQ_MOE_FOLDED_SCALES | LQ_MOE_GENERAL_KERNEL | LQ_MOE_WIDE_KERNEL))
+    return fail(LQ_ERR_VALUE, "moe_forward: unknown flags");
+  if ((flags & LQ_MOE_WIDE_KERNEL) && (flags & LQ_MOE_GENERAL_KERNEL))
+    return fail(LQ_ERR_VALUE, "moe_forward: LQ_MOE_WIDE_KERNEL and LQ_MOE_GENERAL_KERNEL exclude each other");
+  if ((flags & LQ_MOE_WIDE_KERNEL) && !wide_eligible(H, I, flags))
+    return fail(LQ_ERR_UNSUPPORTED,
+                "moe_forward: the wide kernels need hidden % 256 == 0, intermediate % 128 == 0 and exact weights "
+                "(no LQ_MOE_FOLDED_SCALES)");
   if (H % kR2 != 0 || I % kF1 != 0)
     return fail(LQ_ERR_UNSUPPORTED, "moe_forward: needs hidden % 128 == 0 and intermediate % 64 == 0");
   const int64_t g1 = effective_group(H, group_w1);
@@ -1636,10 +1955,59 @@ int launch_general(const MoeArgs &a, int64_t max_g1, int64_t max_g2, hipStream_t
   return LQ_OK;
 }
 
+// persistent grid of the wide kernels: resident workgroups (a multiple of 8),
+// no more than the items can use
+template <int BITS, bool FIRST, bool G128>
+int wide_grid(int64_t max_items) {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int g = cached[dev];
+  if (g == 0) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, moe_wide_kernel<BITS, FIRST, G128>, kWThreads, 0) !=
+            hipSuccess ||
+        per_cu <= 0)
+      per_cu = 1;
+    g = device_info().cus * per_cu;
+    cached[dev] = g;
+  }
+  const int64_t want = (std::max<int64_t>(max_items, 1) + 7) / 8 * 8;
+  return static_cast<int>(std::max<int64_t>(8, std::min<int64_t>(g / 8 * 8, want)));
+}
+
+template <int BITS>
+int launch_wide(const MoeArgs &a, int64_t max_blocks, hipStream_t st, ProfileMarks &pm, int first) {
+  const int64_t max_g1 = max_blocks * (a.I / kWF1), max_g2 = max_blocks * (a.H / kWR2);
+  if (a.g1 == kKC)
+    moe_wide_kernel<BITS, true, true><<<wide_grid<BITS, true, true>(max_g1), kWThreads, 0, st>>>(a);
+  else
+    moe_wide_kernel<BITS, true, false><<<wide_grid<BITS, true, false>(max_g1), kWThreads, 0, st>>>(a);
+  int rc = check_launch("moe_wide_gemm1");
+  if (rc) return rc;
+  pm.mark(first + 1);
+  if (a.g2 == kKC)
+    moe_wide_kernel<BITS, false, true><<<wide_grid<BITS, false, true>(max_g2), kWThreads, 0, st>>>(a);
+  else
+    moe_wide_kernel<BITS, false, false><<<wide_grid<BITS, false, false>(max_g2), kWThreads, 0, st>>>(a);
+  rc = check_launch("moe_wide_gemm2");
+  if (rc) return rc;
+  pm.mark(first + 2);
+  return LQ_OK;
+}
+
 template <int BITS, bool FOLDED>
 int launch_phases(const MoeArgs &a, int64_t max_g1, int64_t max_g2, hipStream_t st, ProfileMarks &pm, int first,
-                  bool stream, bool inplan) {
-  if (stream) {
+                  Path path, bool inplan) {
+  if (path == Path::kWide) {
+    if constexpr (FOLDED) {
+      return fail(LQ_ERR_UNSUPPORTED, "moe_forward: the wide kernels take exact weights only");
+    } else {
+      const int64_t max_blocks = std::min<int64_t>(a.E, a.T * a.k) + a.T * a.k / kWRows;
+      int rc = launch_wide<BITS>(a, max_blocks, st, pm, first);
+      if (rc) return rc;
+    }
+  } else if (path == Path::kStream) {
     int rc = launch_stream<BITS, FOLDED, true>(a, st, inplan);
     if (rc) return rc;
     pm.mark(first + 1);
@@ -1672,14 +2040,17 @@ PlanArgs plan_args(const int32_t *topk_ids, int64_t T, int E, int k, char *ws, c
   p.blocks = reinterpret_cast<int4 *>(ws + w.blocks);
   p.srow = reinterpret_cast<int32_t *>(ws + w.srow);
   p.k = k;
+  p.block_rows = kRowsMax;
   p.hdr = reinterpret_cast<PlanHeader *>(ws + w.hdr);
   return p;
 }
 
-// does this layer run on the streaming GEMMs?
-bool uses_stream(int bits, int H, int I, int64_t group_w1, int64_t group_w2, int flags) {
-  return !(flags & LQ_MOE_GENERAL_KERNEL) &&
-         stream_eligible(bits, H, I, effective_group(H, group_w1), effective_group(I, group_w2));
+Path choose_path(int bits, int64_t T, int H, int I, int E, int k, int64_t group_w1, int64_t group_w2, int flags) {
+  if (flags & LQ_MOE_WIDE_KERNEL) return Path::kWide;  // (validate_layer checked wide_eligible)
+  if (flags & LQ_MOE_GENERAL_KERNEL) return Path::kGeneral;
+  if (wide_eligible(H, I, flags) && T * k >= static_cast<int64_t>(kWideMinRows) * E) return Path::kWide;
+  if (stream_eligible(bits, H, I, effective_group(H, group_w1), effective_group(I, group_w2))) return Path::kStream;
+  return Path::kGeneral;
 }
 
 // [x permute] -> [plan] -> G1 -> G2 -> combine.  The streaming GEMMs stage
@@ -1695,9 +2066,11 @@ int moe_forward_impl(const void *x, bool x_permuted, int64_t T, int H, int I, in
   const int64_t g2 = effective_group(I, group_w2);
   // the folded form applies one scale per 128-wide K chunk
   const bool folded = (flags & LQ_MOE_FOLDED_SCALES) && g1 % kKC == 0 && g2 % kKC == 0;
-  const bool stream = uses_stream(bits, H, I, group_w1, group_w2, flags);
+  const Path path = choose_path(bits, T, H, I, E, k, group_w1, group_w2, flags);
+  const bool stream = path == Path::kStream;
 
-  const PlanArgs p = plan_args(topk_ids, T, E, k, ws, w);
+  PlanArgs p = plan_args(topk_ids, T, E, k, ws, w);
+  if (path == Path::kWide) p.block_rows = kWRows;
   uint16_t *xperm = reinterpret_cast<uint16_t *>(ws + w.xperm);
   if (!stream && !x_permuted) {
     const int64_t n8 = T * H / 8;
@@ -1749,11 +2122,11 @@ int moe_forward_impl(const void *x, bool x_permuted, int64_t T, int H, int I, in
   const int64_t blocks = max_blocks_for(T, E, k);
   const int64_t max_g1 = blocks * (I / kF1), max_g2 = blocks * (H / kR2);
   if (bits == 4)
-    rc = folded ? launch_phases<4, true>(a, max_g1, max_g2, st, pm, first_mark, stream, inplan)
-                : launch_phases<4, false>(a, max_g1, max_g2, st, pm, first_mark, stream, inplan);
+    rc = folded ? launch_phases<4, true>(a, max_g1, max_g2, st, pm, first_mark, path, inplan)
+                : launch_phases<4, false>(a, max_g1, max_g2, st, pm, first_mark, path, inplan);
   else
-    rc = folded ? launch_phases<8, true>(a, max_g1, max_g2, st, pm, first_mark, stream, inplan)
-                : launch_phases<8, false>(a, max_g1, max_g2, st, pm, first_mark, stream, inplan);
+    rc = folded ? launch_phases<8, true>(a, max_g1, max_g2, st, pm, first_mark, path, inplan)
+                : launch_phases<8, false>(a, max_g1, max_g2, st, pm, first_mark, path, inplan);
   if (rc) return rc;
   return pm.rc;
 }
@@ -1777,6 +2150,7 @@ int launch_permute(const int32_t *ids, int64_t N, int E, int32_t *counts, int32_
   p.offsets = offsets;
   p.sorted = sorted;
   p.blocks = nullptr;
+  p.block_rows = kRowsMax;
   p.srow = nullptr;
   p.k = 1;
   plan_kernel<<<1, kPlanBlock, 0, st>>>(p);
@@ -1830,7 +2204,7 @@ extern "C" int lq_moe_layer(const void *x, const void *logits, int logits_dtype,
   int32_t *ids = topk_ids_out ? topk_ids_out : reinterpret_cast<int32_t *>(ws + w.ids);
   float *weights = reinterpret_cast<float *>(ws + w.weights);
   pm.mark(0);
-  const bool streaming = uses_stream(bits, H, I, group_w1, group_w2, flags);
+  const bool streaming = choose_path(bits, T, H, I, E, k, group_w1, group_w2, flags) == Path::kStream;
   // the general GEMMs stage the K-slot permuted copy of x the router writes
   rc = launch_route_topk(logits, logits_dtype, T, E, k, renormalize, ids, weights, st,
                          static_cast<const uint16_t *>(x), H,

@@ -56,6 +56,7 @@ def fused_moe_packed(
     workspace: Optional[torch.Tensor] = None,
     folded_scales: bool = False,
     general_kernel: bool = False,
+    wide_kernel: bool = False,
 ) -> torch.Tensor:
     """The layer on explicit operands: ``x [T, H]`` bf16, int32 ids and fp32 weights ``[T, k]``.
 
@@ -65,7 +66,9 @@ def fused_moe_packed(
     dot product: cheaper, but without the per-weight BF16 rounding the output
     moves by about the reference tolerance (mean-relative ~5e-3).
     ``general_kernel`` runs the general GEMM kernels even where the streaming
-    ones apply (same results bit for bit; for comparison).
+    ones apply, ``wide_kernel`` the wide (matrix-core) ones, which layers with
+    at least 128 routed rows per expert on average take by themselves (same
+    results bit for bit; for comparison).
     """
     g1, g2, I = _check_weights(x, w1, w2)
     T, H = x.shape
@@ -88,7 +91,9 @@ def fused_moe_packed(
         with torch.cuda.device(device):
             rc = lib.lq_moe_forward(
                 _lib.ptr(xc), T, H, I, E, k, _lib.ptr(q1), _lib.ptr(s1), _lib.ptr(q2), _lib.ptr(s2), w1.bits, g1, g2,
-                _moe_flags(folded_scales) | (_lib.LQ_MOE_GENERAL_KERNEL if general_kernel else 0),
+                _moe_flags(folded_scales)
+                | (_lib.LQ_MOE_GENERAL_KERNEL if general_kernel else 0)
+                | (_lib.LQ_MOE_WIDE_KERNEL if wide_kernel else 0),
                 _lib.ptr(ids), _lib.ptr(wts), _lib.ptr(workspace), workspace.numel(),
                 _lib.ptr(out), _lib.stream(device),
             )

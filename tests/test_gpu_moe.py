@@ -213,6 +213,53 @@ def test_streaming_kernels_match_general_kernels(dev, bits, folded, T, k, skew):
     assert_close(a, oracle_out(x, q1, q2, ids, w), bar(folded))
 
 
+@pytest.mark.parametrize("bits,group", [(4, 128), (8, 128), (4, 64)])
+@pytest.mark.parametrize("T,k,skew", [(300, 8, False), (97, 4, True), (20, 2, False)])
+def test_wide_kernels_match_general_kernels(dev, bits, group, T, k, skew):
+    """The wide GEMMs (blocks of up to 128 rows, four weight tiles per wave) do the
+    general kernels' per-chunk arithmetic in the same order, so the two agree bit for
+    bit.  Cases: blocks of <= 32, 33..64 and 65..128 rows, experts spanning several
+    blocks, empty experts, one scale per 128-wide chunk (group 128) or per lane (64)."""
+    E, H, I = 16, 512, 256
+    q1, q2 = make_layer(dev, E, H, I, bits, group=group, seed=T + bits + group)
+    g = torch.Generator().manual_seed(T + 1)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    logits = zipf_logits(T, E, seed=T) if skew else torch.randn(T, E, generator=g)
+    ids, w = route_topk(logits.to(dev), k)
+    a = fused_moe_packed(x, q1, q2, ids, w, wide_kernel=True)
+    b = fused_moe_packed(x, q1, q2, ids, w, general_kernel=True)
+    assert torch.equal(a, b)
+    assert_close(a, oracle_out(x, q1, q2, ids, w))
+
+
+def test_wide_kernels_are_chosen_for_many_rows_per_expert(dev):
+    """At >= 128 routed rows per expert on average the layer takes the wide GEMMs by
+    itself (here exactly 128: 512 tokens x top-2 over 8 experts)."""
+    E, H, I, T, k = 8, 1024, 512, 512, 2
+    q1, q2 = make_layer(dev, E, H, I, 4, seed=21, search="mse")
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    ids, w = route_topk(torch.randn(T, E, generator=g).to(dev), k)
+    a = fused_moe_packed(x, q1, q2, ids, w)
+    assert torch.equal(a, fused_moe_packed(x, q1, q2, ids, w, wide_kernel=True))
+    assert torch.equal(a, fused_moe_packed(x, q1, q2, ids, w, general_kernel=True))
+    assert_close(a, oracle_out(x, q1, q2, ids, w))
+
+
+def test_wide_kernel_flag_errors(dev):
+    q1, q2 = make_layer(dev, 4, 256, 128, 4)
+    x = torch.randn(8, 256, device=dev).to(torch.bfloat16)
+    ids = torch.zeros(8, 1, dtype=torch.int32, device=dev)
+    w = torch.ones(8, 1, device=dev)
+    with pytest.raises(ValueError, match="exclude each other"):
+        fused_moe_packed(x, q1, q2, ids, w, wide_kernel=True, general_kernel=True)
+    with pytest.raises(NotImplementedError, match="wide kernels need"):
+        fused_moe_packed(x, q1, q2, ids, w, wide_kernel=True, folded_scales=True)
+    q1, q2 = make_layer(dev, 4, 128, 64, 4, group=64)  # hidden 128 is not a whole wide item
+    with pytest.raises(NotImplementedError, match="wide kernels need"):
+        fused_moe_packed(x[:, :128].contiguous(), q1, q2, ids, w, wide_kernel=True)
+
+
 def test_streaming_one_hot_expert_many_blocks(dev):
     """One expert holds every token: 13 row blocks of one expert, all streamed."""
     q1, q2 = make_layer(dev, 8, 512, 512, 4, seed=15)
