@@ -120,7 +120,7 @@ def kernel_family(cfg, folded, forced):
     if forced != "auto":
         return forced
     E, H, I, k, T = cfg["experts"], cfg["hidden"], cfg["inter"], cfg["top_k"], cfg["tokens"]
-    if not folded and H % 256 == 0 and I % 128 == 0 and T * k >= 128 * E:
+    if not folded and H % 256 == 0 and I % 256 == 0 and T * k >= 128 * E:
         return "wide"
     step = 512 if cfg["bits"] == 4 else 256
     return "stream" if H % step == 0 and I % step == 0 else "general"

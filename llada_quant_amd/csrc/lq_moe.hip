@@ -586,17 +586,16 @@ __global__ __launch_bounds__(kThreads, 3) void moe_gemm_kernel(MoeArgs a) {
 // wide G1 / G2 kernels (the matrix-core regime: hundreds of rows per expert)
 //
 // An item is (row block of up to 128 sorted rows of one expert, slice of
-// weight rows).  Four waves, one per SIMD, so each holds 512 registers (its
-// 128 accumulators in AGPRs); wave w owns four 16-row weight tiles over the
-// whole K -- G1: the gate and up rows of features [32w, 32w + 32) of the
-// slice (128 features per item), so SwiGLU stays lane-local; G2: output
-// rows [64w, 64w + 64) of the slice (256 per item) -- and multiplies each
+// weight rows).  Eight waves, two per SIMD, so one wave's weight arithmetic
+// runs while the other's MFMAs do; wave w owns two 16-row weight tiles over
+// the whole K -- G1: the gate and up rows of features [16w, 16w + 16) of
+// the slice (128 features per item), so SwiGLU stays lane-local; G2: output
+// rows [32w, 32w + 32) of the slice (256 per item) -- and multiplies each
 // dequantized B fragment with up to 8 row tiles staged in LDS.  One
 // dequantization then feeds 128 rows instead of 32, which keeps the weight
 // arithmetic (~18 VALU per 8 weights, 4 cycles each) below the matrix-core
-// time of the fragment (8 x v_mfma_f32_16x16x32_bf16, 16 cycles each), and
-// each A fragment read from LDS feeds four MFMAs.
-// Token rows are staged one 128-wide K chunk at a time by all 256 threads
+// time of the fragment (8 x v_mfma_f32_16x16x32_bf16, 16 cycles each).
+// Token rows are staged one 128-wide K chunk at a time by all 512 threads
 // (double buffered, 32 KB per stage, one barrier per chunk), one chunk
 // ahead; weight codes are loaded two chunks ahead into registers.  The
 // per-chunk arithmetic and its order are chunk_mfma's (wide_chunk), as in
@@ -605,11 +604,12 @@ __global__ __launch_bounds__(kThreads, 3) void moe_gemm_kernel(MoeArgs a) {
 // slices of one block (the same token rows) and the blocks of one expert
 // (the same weights) run at about the same time on one L2.
 // ---------------------------------------------------------------------------
-constexpr int kWWaves = 4;
+constexpr int kWWaves = 8;
 constexpr int kWThreads = 64 * kWWaves;
 constexpr int kWRows = 128;                  // sorted rows per wide row block
-constexpr int kWF1 = kWWaves * 32;           // G1 features per item
-constexpr int kWR2 = kWWaves * 64;           // G2 output rows per item
+constexpr int kWT = 2;                       // weight tiles per wave
+constexpr int kWF1 = kWWaves * 16 * kWT / 2;  // G1 features per item (gate + up tiles)
+constexpr int kWR2 = kWWaves * 16 * kWT;      // G2 output rows per item
 constexpr int kWStage = kWRows * kRowBytes;  // one LDS stage: 128 rows x 128 K bf16
 
 // One 128-wide K chunk of the wide kernels: chunk_mfma's arithmetic in
@@ -685,16 +685,16 @@ __device__ __forceinline__ void wide_item(const MoeArgs &a, int e, int slice, in
                                           unsigned char *lds) {
   static_assert(NRT == 2 || NRT == 4 || NRT == 8, "row tiles per block");
   constexpr int NQ = NRT * 256 / kWThreads;  // staged pieces per thread and chunk: NRT * 16 rows x 16 pieces
-  constexpr int NT = 4;        // weight tiles per wave
+  constexpr int NT = kWT;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int lc = lane & 15;
   const int lg = lane >> 4;
   const int K = FIRST ? a.H : a.I;
-  const int nk = K / kKC;  // K is a multiple of 128 on this path (host-checked)
+  const int nk = K / kKC;  // K is a multiple of 256 on this path (host-checked): nk is even
 
-  // ---- token rows: piece tid + 256 q of a chunk is row r = piece >> 4,
+  // ---- token rows: piece tid + 512 q of a chunk is row r = piece >> 4,
   // 16-byte piece lc of the row's 128 K values, stored at slot lc ^ (r & 15)
   // (the XOR swizzle chunk_mfma reads).  Rows arrive K-slot permuted (xperm,
   // act); rows past the block re-read its first row and are never stored out.
@@ -721,9 +721,9 @@ __device__ __forceinline__ void wide_item(const MoeArgs &a, int e, int slice, in
     for (int q = 0; q < NQ; ++q) *reinterpret_cast<u32x4 *>(buf + ldsoff[q]) = v[q];
   };
 
-  // ---- weights: tiles c = 0, 1 are gate rows of features 16c + lc of the
-  // wave's 32 (G1), c = 2, 3 the up rows of the same features; G2: output
-  // rows 16c + lc of the wave's 64
+  // ---- weights: tile 0 holds the gate rows of the wave's 16 features
+  // (G1), tile 1 the up rows of the same features; G2: output rows
+  // 16c + lc of the wave's 32
   const int rowbytes = BITS == 4 ? (K >> 1) : K;
   const int G = FIRST ? a.g1 : a.g2;
   const int ng = FIRST ? a.ng1 : a.ng2;
@@ -735,12 +735,12 @@ __device__ __forceinline__ void wide_item(const MoeArgs &a, int e, int slice, in
                                                  static_cast<int64_t>(nrows_w) * ng * 4);
   constexpr int kLaneBytes = BITS == 4 ? 16 : 32;  // one lane's 32 codes of a chunk
   constexpr int kChunkBytes = BITS == 4 ? 64 : 128;
-  const int fbase = slice * kWF1 + 32 * wave;  // G1: the wave's first feature
-  const int obase = slice * kWR2 + 64 * wave;  // G2: the wave's first output row
+  const int fbase = slice * kWF1 + 16 * wave;  // G1: the wave's first feature
+  const int obase = slice * kWR2 + 32 * wave;  // G2: the wave's first output row
   int wvoff[NT], svoff[NT];
 #pragma unroll
   for (int c = 0; c < NT; ++c) {
-    const int wr = FIRST ? (c < 2 ? 0 : a.I) + fbase + 16 * (c & 1) + lc : obase + 16 * c + lc;
+    const int wr = FIRST ? (c == 0 ? 0 : a.I) + fbase + lc : obase + 16 * c + lc;
     wvoff[c] = wr * rowbytes + kLaneBytes * lg;
     svoff[c] = wr * ng * 4;
   }
@@ -770,68 +770,87 @@ __device__ __forceinline__ void wide_item(const MoeArgs &a, int e, int slice, in
   for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
     for (int c = 0; c < NT; ++c) tot[rt][c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-  auto compute = [&](int i, const WChunk<BITS>(&w)[NT], const float(&sc)[NT]) __attribute__((always_inline)) {
-    const unsigned char *buf = lds + (i & 1) * kWStage;
-    if (__all(dq_fast_ok(sc[0]) && dq_fast_ok(sc[1]) && dq_fast_ok(sc[2]) && dq_fast_ok(sc[3])))
-      wide_chunk<BITS, true, NRT, NT>(w, sc, buf, lc, lg, tot);
-    else
-      wide_chunk<BITS, false, NRT, NT>(w, sc, buf, lc, lg, tot);
-  };
-
   // Schedule (loads of a wave complete in issue order):
+  //   first:    the item's scales, for the dequant choice (below)
   //   prologue: tokens 0 -> LDS stage 0, weights 0; tokens 1 -> registers, weights 1
   //   step i:   compute chunk i (weights slot i & 1, LDS stage i & 1);
   //             tokens i+1: registers -> LDS stage (i+1) & 1 (waits for them only:
   //             weights i+1 were issued after them); issue tokens i+2 and
   //             weights i+2 (into slot i & 1); barrier.
-  // Steps past the last chunk compute nothing and load out of range.
-  WChunk<BITS> wb[2][NT];
-  float sb[2][NT];
-  u32x4 av[NQ];
-  load_a(0, av);
-  __builtin_amdgcn_sched_barrier(0);
-  load_w(0, wb[0], sb[0]);
-  __builtin_amdgcn_sched_barrier(0);
-  store_a(0, av);
-  load_a(1, av);
-  __builtin_amdgcn_sched_barrier(0);
-  load_w(1, wb[1], sb[1]);
-  __builtin_amdgcn_sched_barrier(0);
-  __syncthreads();  // chunk 0 staged
-  auto step = [&](int i, auto d_tag) __attribute__((always_inline)) {
-    constexpr int d = decltype(d_tag)::value;
-    if (i < nk) compute(i, wb[d], sb[d]);
-    __builtin_amdgcn_sched_barrier(0);
-    store_a(i + 1, av);
-    load_a(i + 2, av);
-    __builtin_amdgcn_sched_barrier(0);
-    load_w(i + 2, wb[d], sb[d]);
-    __builtin_amdgcn_sched_barrier(0);
-    __syncthreads();  // chunk i consumed by every wave, chunk i + 1 staged
-  };
-  for (int i0 = 0; i0 < nk; i0 += 2) {
-    step(i0, std::integral_constant<int, 0>{});
-    step(i0 + 1, std::integral_constant<int, 1>{});
+  // The chunk count is even (host-checked), so the loop is straight-line;
+  // the two steps past the last chunk load out of range.
+  // Dequant choice: one per item and wave (FAST needs dq_fast_ok for every
+  // scale the wave meets), so each K loop holds one form only.  Lane group
+  // lg checks groups lg, lg + 4, ... of its tiles' rows, up to 4 * kChk
+  // groups; longer rows take the exact-slow form throughout.
+  constexpr int kChk = G128 ? 4 : 8;
+  bool ok = ng <= 4 * kChk;
+  {
+    const __amdgpu_buffer_rsrc_t rs = ok ? srsrc : empty;
+    float chk[NT][kChk];
+#pragma unroll
+    for (int c = 0; c < NT; ++c)
+#pragma unroll
+      for (int j = 0; j < kChk; ++j)  // groups past the row read as 0 (fast)
+        chk[c][j] = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(lg + 4 * j < ng ? rs : empty, svoff[c], 4 * (lg + 4 * j), 0));
+#pragma unroll
+    for (int c = 0; c < NT; ++c)
+#pragma unroll
+      for (int j = 0; j < kChk; ++j) ok = ok && dq_fast_ok(chk[c][j]);
   }
+  // prologue and K loop, one copy per dequant form
+  auto kloop = [&](auto fast_tag) __attribute__((always_inline)) {
+    constexpr bool FAST = decltype(fast_tag)::value;
+    WChunk<BITS> wb[2][NT];
+    float sb[2][NT];
+    u32x4 av[NQ];
+    load_a(0, av);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(0, wb[0], sb[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    store_a(0, av);
+    load_a(1, av);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(1, wb[1], sb[1]);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();  // chunk 0 staged
+    auto step = [&](int i, auto d_tag) __attribute__((always_inline)) {
+      constexpr int d = decltype(d_tag)::value;
+      wide_chunk<BITS, FAST, NRT, NT>(wb[d], sb[d], lds + (i & 1) * kWStage, lc, lg, tot);
+      __builtin_amdgcn_sched_barrier(0);
+      store_a(i + 1, av);
+      load_a(i + 2, av);
+      __builtin_amdgcn_sched_barrier(0);
+      load_w(i + 2, wb[d], sb[d]);
+      __builtin_amdgcn_sched_barrier(0);
+      __syncthreads();  // chunk i consumed by every wave, chunk i + 1 staged
+    };
+    for (int i0 = 0; i0 < nk; i0 += 2) {
+      step(i0, std::integral_constant<int, 0>{});
+      step(i0 + 1, std::integral_constant<int, 1>{});
+    }
+  };
+  if (__all(ok))
+    kloop(std::true_type{});
+  else
+    kloop(std::false_type{});
 
   if constexpr (FIRST) {
     // reference op order (INFERENCE_REPO_CHANGES.md:296-309): g, u -> bf16;
     // silu in fp32 -> bf16; bf16 product; act stored K-slot permuted
+    const int f = kslot(fbase + lc);
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int f = kslot(fbase + 16 * c + lc);
+    for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
-      for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int m = rt * 16 + 4 * lg + j;
-          if (m < rows) {
-            const float gb = bf16_round(tot[rt][c][j]);
-            const float ub = bf16_round(tot[rt][c + 2][j]);
-            a.act[static_cast<int64_t>(row0 + m) * a.I + f] = static_cast<uint16_t>(swiglu_pk(gb, 0.0f, ub, 0.0f));
-          }
+      for (int j = 0; j < 4; ++j) {
+        const int m = rt * 16 + 4 * lg + j;
+        if (m < rows) {
+          const float gb = bf16_round(tot[rt][0][j]);
+          const float ub = bf16_round(tot[rt][1][j]);
+          a.act[static_cast<int64_t>(row0 + m) * a.I + f] = static_cast<uint16_t>(swiglu_pk(gb, 0.0f, ub, 0.0f));
         }
-    }
+      }
   } else {
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt)
@@ -855,6 +874,7 @@ __device__ __forceinline__ void wide_item(const MoeArgs &a, int e, int slice, in
 // workgroups.
 template <int BITS, bool FIRST, bool G128>
 __global__ __launch_bounds__(kWThreads, 1) void moe_wide_kernel(MoeArgs a) {
+  static_assert(kWT == 2, "G1 pairs the gate and up tile of each wave");
   __shared__ __align__(16) unsigned char lds[2 * kWStage];
   const int nb = __builtin_amdgcn_readfirstlane(a.hdr->n_blk);
   const int per = FIRST ? a.I / kWF1 : a.H / kWR2;
@@ -1798,10 +1818,11 @@ struct ProfileMarks {
 enum class Path { kStream, kGeneral, kWide };
 constexpr int kWideMinRows = 128;
 
-// the wide kernels need whole items along N (128 features, 256 output rows)
-// and exact weights (the folded form keeps its own kernels)
+// the wide kernels need whole items along N (128 features, 256 output
+// rows), whole pairs of 128-wide K chunks, and exact weights (the folded
+// form keeps its own kernels)
 bool wide_eligible(int H, int I, int flags) {
-  return H % kWR2 == 0 && I % kWF1 == 0 && !(flags & LQ_MOE_FOLDED_SCALES);
+  return H % kWR2 == 0 && I % kWR2 == 0 && !(flags & LQ_MOE_FOLDED_SCALES);
 }
 
 int validate_layer(const void *x, int64_t T, int H, int I, int E, int k, const int8_t *q1, const float *s1,
@@ -1818,7 +1839,7 @@ int validate_layer(const void *x, int64_t T, int H, int I, int E, int k, const i
     return fail(LQ_ERR_VALUE, "moe_forward: LQ_MOE_WIDE_KERNEL and LQ_MOE_GENERAL_KERNEL exclude each other");
   if ((flags & LQ_MOE_WIDE_KERNEL) && !wide_eligible(H, I, flags))
     return fail(LQ_ERR_UNSUPPORTED,
-                "moe_forward: the wide kernels need hidden % 256 == 0, intermediate % 128 == 0 and exact weights "
+                "moe_forward: the wide kernels need hidden % 256 == 0, intermediate % 256 == 0 and exact weights "
                 "(no LQ_MOE_FOLDED_SCALES)");
   if (H % kR2 != 0 || I % kF1 != 0)
     return fail(LQ_ERR_UNSUPPORTED, "moe_forward: needs hidden % 128 == 0 and intermediate % 64 == 0");
