@@ -1607,82 +1607,56 @@ struct PlanArgs {
   PlanHeader *hdr;
 };
 
-// the plan for one workgroup of kPlanBlock threads; id_at(a) returns the
-// expert of assignment a (read from memory or from LDS)
+// Block table from the expert counts cnt[] and their exclusive offsets
+// off[] (LDS): blocks of at most p.block_rows sorted rows, expert-major;
+// nbs (E + 1 entries) and tmp (E) are LDS scratch.  Every thread of the
+// workgroup calls it.
+__device__ __forceinline__ void plan_blocks(const PlanArgs &p, const int *cnt, const int *off, int *nbs, int *tmp) {
+  const int tid = threadIdx.x;
+  const int E = p.E;
+  const int br = p.block_rows;
+  for (int e = tid; e < E; e += kPlanBlock) tmp[e] = (cnt[e] + br - 1) / br;
+  __syncthreads();
+  if ((tid >> 6) == 0) wave0_exclusive_scan(tmp, nbs, E, &nbs[E]);
+  __syncthreads();
+  // block b of expert e covers sorted rows [off[e] + br j, + br) with j = b - nbs[e]
+  const int nb_total = nbs[E];
+  for (int b = tid; b < nb_total; b += kPlanBlock) {
+    int lo = 0, hi = E;  // largest e with nbs[e] <= b
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (nbs[mid] <= b) lo = mid;
+      else hi = mid;
+    }
+    const int e = lo;
+    const int r0 = off[e] + (b - nbs[e]) * br;
+    p.blocks[b] = make_int4(e, r0, min(br, off[e] + cnt[e] - r0), 0);
+  }
+  if (tid == 0) p.hdr->n_blk = nb_total;
+  __syncthreads();
+}
+
+// Stable scatter of assignments [a_begin, a_end): chunks of kPlanBlock
+// assignments in order; within a chunk, rank = peers with the same expert
+// in lower lanes of this wave + peers in lower waves.  base[e] (LDS) is the
+// sorted position of expert e's next assignment and advances; wcnt (LDS,
+// zero on entry and on exit) holds per-wave counts.
 template <class IdAt>
-__device__ __forceinline__ void plan_body(const PlanArgs &p, IdAt id_at) {
-  __shared__ int hist[kMaxExperts];
-  __shared__ int base[kMaxExperts];
-  __shared__ int nbs[kMaxExperts + 1];  // exclusive scan of row blocks per expert
-  __shared__ int wcnt[kPlanWaves][kMaxExperts];
-  __shared__ int total;
+__device__ __forceinline__ void plan_scatter(const PlanArgs &p, IdAt id_at, int *base, int (*wcnt)[kMaxExperts],
+                                             int64_t a_begin, int64_t a_end) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int E = p.E;
-  for (int e = tid; e < kMaxExperts; e += kPlanBlock) hist[e] = 0;
-  for (int i = tid; i < kPlanWaves * kMaxExperts; i += kPlanBlock) (&wcnt[0][0])[i] = 0;
-  __syncthreads();
-  // (8 ids per thread in flight at once: the loop is latency-bound otherwise)
-  for (int64_t a0 = 0; a0 < p.N; a0 += 8 * kPlanBlock) {
-    int idv[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int64_t a = a0 + j * kPlanBlock + tid;
-      idv[j] = a < p.N ? id_at(a) : -1;
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (idv[j] >= 0 && idv[j] < E) atomicAdd(&hist[idv[j]], 1);
-  }
-  __syncthreads();
-  if (wave == 0) wave0_exclusive_scan(hist, base, E, &total);
-  __syncthreads();
-  for (int e = tid; e < E; e += kPlanBlock) {
-    p.counts[e] = hist[e];
-    p.offsets[e] = base[e];
-  }
-  if (tid == 0) p.offsets[E] = total;
-
-  if (p.blocks != nullptr) {
-    // row blocks per expert and their scan
-    const int br = p.block_rows;
-    for (int e = tid; e < E; e += kPlanBlock) wcnt[0][e] = (hist[e] + br - 1) / br;
-    __syncthreads();
-    if (wave == 0) wave0_exclusive_scan(wcnt[0], nbs, E, &nbs[E]);
-    __syncthreads();
-    // block table, expert-major: block b of expert e covers sorted rows
-    // [offsets[e] + br j, + br) with j = b - nbs[e]
-    const int nb_total = nbs[E];
-    for (int b = tid; b < nb_total; b += kPlanBlock) {
-      int lo = 0, hi = E;  // largest e with nbs[e] <= b
-      while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (nbs[mid] <= b) lo = mid;
-        else hi = mid;
-      }
-      const int e = lo;
-      const int r0 = base[e] + (b - nbs[e]) * br;
-      p.blocks[b] = make_int4(e, r0, min(br, base[e] + hist[e] - r0), 0);
-    }
-    if (tid == 0) p.hdr->n_blk = nb_total;
-    __syncthreads();
-    for (int e = tid; e < E; e += kPlanBlock) wcnt[0][e] = 0;
-  }
-  __syncthreads();
-
-  // stable scatter: chunks of kPlanBlock assignments in order; within a
-  // chunk, rank = peers with the same expert in lower lanes of this wave +
-  // peers in lower waves
   int nbits = 1;
   while ((1 << nbits) <= E) ++nbits;
   const unsigned long long lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   // the next chunk's id is loaded while this chunk is ranked and scattered
-  int next = tid < p.N ? id_at(tid) : -1;
-  for (int64_t chunk = 0; chunk < p.N; chunk += kPlanBlock) {
+  int next = a_begin + tid < a_end ? id_at(a_begin + tid) : -1;
+  for (int64_t chunk = a_begin; chunk < a_end; chunk += kPlanBlock) {
     const int64_t a = chunk + tid;
     const int raw = next;
-    next = a + kPlanBlock < p.N ? id_at(a + kPlanBlock) : -1;
+    next = a + kPlanBlock < a_end ? id_at(a + kPlanBlock) : -1;
     const bool valid = raw >= 0 && raw < E;
     const int key = valid ? raw : E;
     unsigned long long peers = ~0ull;
@@ -1713,6 +1687,120 @@ __device__ __forceinline__ void plan_body(const PlanArgs &p, IdAt id_at) {
   }
 }
 
+// the plan for one workgroup of kPlanBlock threads; id_at(a) returns the
+// expert of assignment a (read from memory or from LDS)
+template <class IdAt>
+__device__ __forceinline__ void plan_body(const PlanArgs &p, IdAt id_at) {
+  __shared__ int hist[kMaxExperts];
+  __shared__ int base[kMaxExperts];
+  __shared__ int nbs[kMaxExperts + 1];  // exclusive scan of row blocks per expert
+  __shared__ int wcnt[kPlanWaves][kMaxExperts];
+  __shared__ int total;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int E = p.E;
+  for (int e = tid; e < kMaxExperts; e += kPlanBlock) hist[e] = 0;
+  for (int i = tid; i < kPlanWaves * kMaxExperts; i += kPlanBlock) (&wcnt[0][0])[i] = 0;
+  __syncthreads();
+  // (8 ids per thread in flight at once: the loop is latency-bound otherwise)
+  for (int64_t a0 = 0; a0 < p.N; a0 += 8 * kPlanBlock) {
+    int idv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t a = a0 + j * kPlanBlock + tid;
+      idv[j] = a < p.N ? id_at(a) : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (idv[j] >= 0 && idv[j] < E) atomicAdd(&hist[idv[j]], 1);
+  }
+  __syncthreads();
+  if (wave == 0) wave0_exclusive_scan(hist, base, E, &total);
+  __syncthreads();
+  for (int e = tid; e < E; e += kPlanBlock) {
+    p.counts[e] = hist[e];
+    p.offsets[e] = base[e];
+  }
+  if (tid == 0) p.offsets[E] = total;
+  if (p.blocks != nullptr) plan_blocks(p, hist, base, nbs, wcnt[0]);
+  for (int e = tid; e < E; e += kPlanBlock) wcnt[0][e] = 0;
+  __syncthreads();
+  plan_scatter(p, id_at, base, wcnt, 0, p.N);
+}
+
+// Multi-workgroup plan for large layers, two launches with the same result
+// as plan_kernel.  Segment s is assignments [s kPlanSeg, (s+1) kPlanSeg).
+// plan_count_kernel: workgroup s writes its segment's expert counts to
+// seg_cnt[s][E].  plan_scatter_kernel: workgroup s adds up every segment's
+// counts (the totals) and those of the segments before it (its prefix),
+// scans the totals into offsets, and scatters its own segment stably from
+// offsets + prefix; workgroup 0 also writes counts, offsets and the block
+// table.
+constexpr int kPlanSeg = 4 * kPlanBlock;
+
+__global__ __launch_bounds__(kPlanBlock) void plan_count_kernel(PlanArgs p, int32_t *seg_cnt) {
+  __shared__ int hist[kMaxExperts];
+  const int tid = threadIdx.x;
+  const int E = p.E;
+  for (int e = tid; e < E; e += kPlanBlock) hist[e] = 0;
+  __syncthreads();
+  const int64_t a0 = static_cast<int64_t>(blockIdx.x) * kPlanSeg;
+  int idv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t a = a0 + j * kPlanBlock + tid;
+    idv[j] = a < p.N ? p.ids[a] : -1;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (idv[j] >= 0 && idv[j] < E) atomicAdd(&hist[idv[j]], 1);
+  __syncthreads();
+  for (int e = tid; e < E; e += kPlanBlock) seg_cnt[static_cast<int64_t>(blockIdx.x) * E + e] = hist[e];
+}
+
+__global__ __launch_bounds__(kPlanBlock) void plan_scatter_kernel(PlanArgs p, const int32_t *seg_cnt, int nseg) {
+  __shared__ int tot[kMaxExperts];
+  __shared__ int base[kMaxExperts];
+  __shared__ int pre[kMaxExperts];
+  __shared__ int nbs[kMaxExperts + 1];
+  __shared__ int wcnt[kPlanWaves][kMaxExperts];
+  __shared__ int total;
+  const int tid = threadIdx.x;
+  const int E = p.E;
+  const int seg = blockIdx.x;
+  for (int e = tid; e < E; e += kPlanBlock) {
+    tot[e] = 0;
+    pre[e] = 0;
+  }
+  for (int i = tid; i < kPlanWaves * kMaxExperts; i += kPlanBlock) (&wcnt[0][0])[i] = 0;
+  __syncthreads();
+  const int64_t n_cnt = static_cast<int64_t>(nseg) * E;
+  for (int64_t i = tid; i < n_cnt; i += kPlanBlock) {
+    const int c = seg_cnt[i];
+    const int e = static_cast<int>(i % E);
+    if (c) {
+      atomicAdd(&tot[e], c);
+      if (i / E < seg) atomicAdd(&pre[e], c);
+    }
+  }
+  __syncthreads();
+  if ((tid >> 6) == 0) wave0_exclusive_scan(tot, base, E, &total);
+  __syncthreads();
+  if (seg == 0) {
+    for (int e = tid; e < E; e += kPlanBlock) {
+      p.counts[e] = tot[e];
+      p.offsets[e] = base[e];
+    }
+    if (tid == 0) p.offsets[E] = total;
+    if (p.blocks != nullptr) plan_blocks(p, tot, base, nbs, wcnt[0]);
+    for (int e = tid; e < E; e += kPlanBlock) wcnt[0][e] = 0;
+  }
+  for (int e = tid; e < E; e += kPlanBlock) base[e] += pre[e];
+  __syncthreads();
+  const int64_t a_begin = static_cast<int64_t>(seg) * kPlanSeg;
+  plan_scatter(p, [&](int64_t a) { return p.ids[a]; }, base, wcnt, a_begin, min(p.N, a_begin + kPlanSeg));
+}
+
 __global__ __launch_bounds__(kPlanBlock) void plan_kernel(PlanArgs p) {
   plan_body(p, [&](int64_t a) { return p.ids[a]; });
 }
@@ -1730,7 +1818,7 @@ __global__ __launch_bounds__(256) void permute_rows_kernel(const uint16_t *__res
 // ---------------------------------------------------------------------------
 
 struct WsLayout {
-  size_t counts, offsets, sorted, srow, hdr, blocks, slotplan, slotasg, ids, weights, xperm, act, ybuf, total;
+  size_t counts, offsets, sorted, srow, hdr, blocks, slotplan, slotasg, segcnt, ids, weights, xperm, act, ybuf, total;
 };
 
 inline size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
@@ -1760,6 +1848,7 @@ WsLayout ws_layout(int64_t T, int H, int I, int E, int k) {
   take(w.blocks, sizeof(int4) * max_blocks_for(T, E, k));
   take(w.slotplan, sizeof(int4) * kMaxSlots);
   take(w.slotasg, sizeof(int32_t) * kMaxSlots * kRowsMax);
+  take(w.segcnt, sizeof(int32_t) * E * ((N + kPlanSeg - 1) / kPlanSeg));  // multi-workgroup plan
   take(w.ids, sizeof(int32_t) * N);
   take(w.weights, sizeof(float) * N);
   take(w.xperm, sizeof(uint16_t) * T * H);
@@ -2106,8 +2195,18 @@ int moe_forward_impl(const void *x, bool x_permuted, int64_t T, int H, int I, in
       stream && T * k <= kPlanMaxN && nb_max <= device_info().cus && device_info().cus <= kMaxSlots;
   int rc = LQ_OK;
   if (!inplan) {
-    plan_kernel<<<1, kPlanBlock, 0, st>>>(p);
-    rc = check_launch("moe_plan");
+    const int64_t nseg = ceil_div(T * k, kPlanSeg);
+    if (nseg > 1) {  // large layers: one workgroup per segment of assignments
+      int32_t *segcnt = reinterpret_cast<int32_t *>(ws + w.segcnt);
+      plan_count_kernel<<<static_cast<int>(nseg), kPlanBlock, 0, st>>>(p, segcnt);
+      rc = check_launch("moe_plan_count");
+      if (rc) return rc;
+      plan_scatter_kernel<<<static_cast<int>(nseg), kPlanBlock, 0, st>>>(p, segcnt, static_cast<int>(nseg));
+      rc = check_launch("moe_plan_scatter");
+    } else {
+      plan_kernel<<<1, kPlanBlock, 0, st>>>(p);
+      rc = check_launch("moe_plan");
+    }
     if (rc) return rc;
   }
   pm.mark(first_mark);

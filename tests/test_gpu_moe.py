@@ -246,6 +246,23 @@ def test_wide_kernels_are_chosen_for_many_rows_per_expert(dev):
     assert_close(a, oracle_out(x, q1, q2, ids, w))
 
 
+@pytest.mark.parametrize("T,k,E", [(2600, 4, 8), (1100, 8, 16)])
+def test_multi_workgroup_plan(dev, T, k, E):
+    """More than 4096 routed rows: the expert plan runs as one workgroup per segment
+    of 4096 assignments (count, then scatter); the whole output is checked against
+    the oracle, and the wide, general and streaming GEMMs (all fed by that plan) agree."""
+    H, I = 512, 512
+    q1, q2 = make_layer(dev, E, H, I, 4, seed=T + E)
+    g = torch.Generator().manual_seed(T)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    logits = zipf_logits(T, E, seed=T).to(dev)
+    ids, w = route_topk(logits, k)
+    a = fused_moe_packed(x, q1, q2, ids, w)
+    assert torch.equal(a, fused_moe_packed(x, q1, q2, ids, w, general_kernel=True))
+    assert torch.equal(a, fused_moe_packed(x, q1, q2, ids, w, wide_kernel=True))
+    assert_close(a, oracle_out(x, q1, q2, ids, w))
+
+
 def test_wide_kernel_flag_errors(dev):
     q1, q2 = make_layer(dev, 4, 256, 128, 4)
     x = torch.randn(8, 256, device=dev).to(torch.bfloat16)
