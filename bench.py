@@ -66,6 +66,7 @@ def parse_args():
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--kernel", choices=("auto", "stream", "general", "wide"), default="auto",
                    help="GEMM family (auto: the library's own choice for the shape)")
+    p.add_argument("--tokens", type=int, default=0, help="override the configuration's token count")
     p.add_argument("--folded", action="store_true",
                    help="time the LQ_MOE_FOLDED_SCALES form (integer codes, fp32 group scale) as the headline")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -120,7 +121,7 @@ def kernel_family(cfg, folded, forced):
     if forced != "auto":
         return forced
     E, H, I, k, T = cfg["experts"], cfg["hidden"], cfg["inter"], cfg["top_k"], cfg["tokens"]
-    if not folded and H % 256 == 0 and I % 256 == 0 and T * k >= 128 * E:
+    if not folded and H % 256 == 0 and I % 256 == 0 and T * k >= 32 * E:
         return "wide"
     step = 512 if cfg["bits"] == 4 else 256
     return "stream" if H % step == 0 and I % step == 0 else "general"
@@ -304,6 +305,8 @@ def main():
 
     cfg = dict(experts=64, hidden=2048, inter=1024, top_k=8)
     cfg.update(CONFIGS[args.config])
+    if args.tokens:
+        cfg["tokens"] = args.tokens
     E, H, I, k, T = cfg["experts"], cfg["hidden"], cfg["inter"], cfg["top_k"], cfg["tokens"]
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
@@ -377,7 +380,8 @@ def main():
         return stage_ms
 
     family = kernel_family(cfg, args.folded, args.kernel)
-    kflag = {"wide": _lib.LQ_MOE_WIDE_KERNEL, "general": _lib.LQ_MOE_GENERAL_KERNEL}.get(args.kernel, 0)
+    kflag = {"wide": _lib.LQ_MOE_WIDE_KERNEL, "general": _lib.LQ_MOE_GENERAL_KERNEL,
+             "stream": _lib.LQ_MOE_STREAM_KERNEL}.get(args.kernel, 0)
     calls = make_calls((_lib.LQ_MOE_FOLDED_SCALES if args.folded else 0) | kflag)
     wall0 = time.perf_counter()
     ms_per_step = timed(calls, args.steps, args.warmup)
@@ -404,7 +408,7 @@ def main():
     stages["gemm2_gbps"] = round(g2_b / (stage_ms[3] / 1e3) / 1e9, 1)
     # the other weight form (the wide kernels take exact weights only)
     other_calls = make_calls(0 | kflag if args.folded else
-                             _lib.LQ_MOE_FOLDED_SCALES | (kflag if args.kernel == "general" else 0))
+                             _lib.LQ_MOE_FOLDED_SCALES | (kflag if args.kernel in ("general", "stream") else 0))
     other_ms = timed(other_calls, max(10, args.steps // 4), 3)
     other_stage = staged(other_calls, max(10, args.steps // 4))
 

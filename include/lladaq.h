@@ -46,6 +46,7 @@ extern "C" {
 #define LQ_MOE_FOLDED_SCALES 1 /* exact integer codes in the MFMA, group scale in fp32 */
 #define LQ_MOE_GENERAL_KERNEL 2 /* use the general GEMM kernels for every shape (same results) */
 #define LQ_MOE_WIDE_KERNEL 4    /* use the wide (matrix-core) GEMM kernels (same results; H % 256, I % 256) */
+#define LQ_MOE_STREAM_KERNEL 8  /* use the streaming (bandwidth) GEMM kernels (same results; see lq_moe_forward) */
 
 /* scale search codes (QuantConfig.scale_search) */
 #define LQ_SCALE_AMAX 0

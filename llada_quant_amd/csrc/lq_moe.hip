@@ -1901,11 +1901,13 @@ struct ProfileMarks {
   }
 };
 
-// The GEMM family a layer runs on.  Wide: many rows per expert (on average
-// at least kWideMinRows), where the matrix cores bound the layer; streaming:
-// the weight-bandwidth regime; general: every other supported shape.
+// The GEMM family a layer runs on.  Wide: at least kWideMinRows routed rows
+// per expert on average (measured on MI355X at E64 H2048 I1024, INT4 and
+// INT8: the wide kernels win from 32 rows per expert on, the streaming ones
+// at 16); streaming: the weight-bandwidth regime below that; general: every
+// other supported shape.
 enum class Path { kStream, kGeneral, kWide };
-constexpr int kWideMinRows = 128;
+constexpr int kWideMinRows = 32;
 
 // the wide kernels need whole items along N (128 features, 256 output
 // rows), whole pairs of 128-wide K chunks, and exact weights (the folded
@@ -1913,6 +1915,8 @@ constexpr int kWideMinRows = 128;
 bool wide_eligible(int H, int I, int flags) {
   return H % kWR2 == 0 && I % kWR2 == 0 && !(flags & LQ_MOE_FOLDED_SCALES);
 }
+
+bool stream_eligible(int bits, int H, int I, int64_t g1, int64_t g2);
 
 int validate_layer(const void *x, int64_t T, int H, int I, int E, int k, const int8_t *q1, const float *s1,
                    const int8_t *q2, const float *s2, int bits, int64_t group_w1, int64_t group_w2, int flags,
@@ -1922,10 +1926,14 @@ int validate_layer(const void *x, int64_t T, int H, int I, int E, int k, const i
   if (E < 1 || E > kMaxExperts)
     return fail(LQ_ERR_UNSUPPORTED, "moe_forward: 1 <= num_experts <= " + std::to_string(kMaxExperts));
   if (k > E) return fail(LQ_ERR_VALUE, "moe_forward: top_k exceeds num_experts");
-  if (flags & ~(LQ_MOE_FOLDED_SCALES | LQ_MOE_GENERAL_KERNEL | LQ_MOE_WIDE_KERNEL))
+  if (flags & ~(LQ_MOE_FOLDED_SCALES | LQ_MOE_GENERAL_KERNEL | LQ_MOE_WIDE_KERNEL | LQ_MOE_STREAM_KERNEL))
     return fail(LQ_ERR_VALUE, "moe_forward: unknown flags");
-  if ((flags & LQ_MOE_WIDE_KERNEL) && (flags & LQ_MOE_GENERAL_KERNEL))
-    return fail(LQ_ERR_VALUE, "moe_forward: LQ_MOE_WIDE_KERNEL and LQ_MOE_GENERAL_KERNEL exclude each other");
+  {
+    const int forced = flags & (LQ_MOE_GENERAL_KERNEL | LQ_MOE_WIDE_KERNEL | LQ_MOE_STREAM_KERNEL);
+    if (forced & (forced - 1))
+      return fail(LQ_ERR_VALUE,
+                  "moe_forward: LQ_MOE_WIDE_KERNEL, LQ_MOE_STREAM_KERNEL and LQ_MOE_GENERAL_KERNEL exclude each other");
+  }
   if ((flags & LQ_MOE_WIDE_KERNEL) && !wide_eligible(H, I, flags))
     return fail(LQ_ERR_UNSUPPORTED,
                 "moe_forward: the wide kernels need hidden % 256 == 0, intermediate % 256 == 0 and exact weights "
@@ -1946,6 +1954,10 @@ int validate_layer(const void *x, int64_t T, int H, int I, int E, int k, const i
     return fail(LQ_ERR_UNSUPPORTED, "moe_forward: too many tokens for one call");
   if (int64_t{2} * I * H >= kOutOfRange)
     return fail(LQ_ERR_UNSUPPORTED, "moe_forward: one expert's weights exceed 2 GiB");
+  if ((flags & LQ_MOE_STREAM_KERNEL) && !stream_eligible(bits, H, I, g1, g2))
+    return fail(LQ_ERR_UNSUPPORTED,
+                "moe_forward: the streaming kernels need hidden and intermediate in whole 512-wide (INT4) or "
+                "256-wide (INT8) steps, group lengths that are multiples of 128, and K <= the LDS capacity");
   if (max_blocks_for(T, E, k) * (I / kF1 + H / kR2) > 0x3FFFFFFF)
     return fail(LQ_ERR_UNSUPPORTED, "moe_forward: work list too long");
   if (T == 0) return LQ_OK;
@@ -2156,7 +2168,8 @@ PlanArgs plan_args(const int32_t *topk_ids, int64_t T, int E, int k, char *ws, c
 }
 
 Path choose_path(int bits, int64_t T, int H, int I, int E, int k, int64_t group_w1, int64_t group_w2, int flags) {
-  if (flags & LQ_MOE_WIDE_KERNEL) return Path::kWide;  // (validate_layer checked wide_eligible)
+  if (flags & LQ_MOE_WIDE_KERNEL) return Path::kWide;  // (validate_layer checked the forced family)
+  if (flags & LQ_MOE_STREAM_KERNEL) return Path::kStream;
   if (flags & LQ_MOE_GENERAL_KERNEL) return Path::kGeneral;
   if (wide_eligible(H, I, flags) && T * k >= static_cast<int64_t>(kWideMinRows) * E) return Path::kWide;
   if (stream_eligible(bits, H, I, effective_group(H, group_w1), effective_group(I, group_w2))) return Path::kStream;

@@ -26,6 +26,7 @@ ABI_VERSION = 2
 LQ_MOE_FOLDED_SCALES = 1
 LQ_MOE_GENERAL_KERNEL = 2
 LQ_MOE_WIDE_KERNEL = 4
+LQ_MOE_STREAM_KERNEL = 8
 
 DTYPE_CODES = {torch.float32: LQ_F32, torch.float16: LQ_F16, torch.bfloat16: LQ_BF16}
 

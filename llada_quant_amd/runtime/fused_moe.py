@@ -57,6 +57,7 @@ def fused_moe_packed(
     folded_scales: bool = False,
     general_kernel: bool = False,
     wide_kernel: bool = False,
+    stream_kernel: bool = False,
 ) -> torch.Tensor:
     """The layer on explicit operands: ``x [T, H]`` bf16, int32 ids and fp32 weights ``[T, k]``.
 
@@ -67,8 +68,9 @@ def fused_moe_packed(
     moves by about the reference tolerance (mean-relative ~5e-3).
     ``general_kernel`` runs the general GEMM kernels even where the streaming
     ones apply, ``wide_kernel`` the wide (matrix-core) ones, which layers with
-    at least 128 routed rows per expert on average take by themselves (same
-    results bit for bit; for comparison).
+    at least 32 routed rows per expert on average take by themselves, and
+    ``stream_kernel`` the streaming (weight-bandwidth) ones, which smaller
+    layers take (same results bit for bit; for comparison).
     """
     g1, g2, I = _check_weights(x, w1, w2)
     T, H = x.shape
@@ -93,7 +95,8 @@ def fused_moe_packed(
                 _lib.ptr(xc), T, H, I, E, k, _lib.ptr(q1), _lib.ptr(s1), _lib.ptr(q2), _lib.ptr(s2), w1.bits, g1, g2,
                 _moe_flags(folded_scales)
                 | (_lib.LQ_MOE_GENERAL_KERNEL if general_kernel else 0)
-                | (_lib.LQ_MOE_WIDE_KERNEL if wide_kernel else 0),
+                | (_lib.LQ_MOE_WIDE_KERNEL if wide_kernel else 0)
+                | (_lib.LQ_MOE_STREAM_KERNEL if stream_kernel else 0),
                 _lib.ptr(ids), _lib.ptr(wts), _lib.ptr(workspace), workspace.numel(),
                 _lib.ptr(out), _lib.stream(device),
             )

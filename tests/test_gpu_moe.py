@@ -207,7 +207,7 @@ def test_streaming_kernels_match_general_kernels(dev, bits, folded, T, k, skew):
     x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
     logits = zipf_logits(T, E, seed=T) if skew else torch.randn(T, E, generator=g)
     ids, w = route_topk(logits.to(dev), k)
-    a = fused_moe_packed(x, q1, q2, ids, w, folded_scales=folded)
+    a = fused_moe_packed(x, q1, q2, ids, w, folded_scales=folded, stream_kernel=True)
     b = fused_moe_packed(x, q1, q2, ids, w, folded_scales=folded, general_kernel=True)
     assert torch.equal(a, b)
     assert_close(a, oracle_out(x, q1, q2, ids, w), bar(folded))
@@ -232,16 +232,19 @@ def test_wide_kernels_match_general_kernels(dev, bits, group, T, k, skew):
     assert_close(a, oracle_out(x, q1, q2, ids, w))
 
 
-def test_wide_kernels_are_chosen_for_many_rows_per_expert(dev):
-    """At >= 128 routed rows per expert on average the layer takes the wide GEMMs by
-    itself (here exactly 128: 512 tokens x top-2 over 8 experts)."""
-    E, H, I, T, k = 8, 1024, 512, 512, 2
+@pytest.mark.parametrize("T", [128, 124])
+def test_gemm_family_threshold(dev, T):
+    """At >= 32 routed rows per expert on average the layer takes the wide GEMMs by
+    itself, below that the streaming ones (T=128: exactly 32 rows per expert over 8
+    experts at top-2; T=124: 31); every family gives the same bits."""
+    E, H, I, k = 8, 1024, 512, 2
     q1, q2 = make_layer(dev, E, H, I, 4, seed=21, search="mse")
     g = torch.Generator().manual_seed(21)
     x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
     ids, w = route_topk(torch.randn(T, E, generator=g).to(dev), k)
     a = fused_moe_packed(x, q1, q2, ids, w)
     assert torch.equal(a, fused_moe_packed(x, q1, q2, ids, w, wide_kernel=True))
+    assert torch.equal(a, fused_moe_packed(x, q1, q2, ids, w, stream_kernel=True))
     assert torch.equal(a, fused_moe_packed(x, q1, q2, ids, w, general_kernel=True))
     assert_close(a, oracle_out(x, q1, q2, ids, w))
 
@@ -259,7 +262,7 @@ def test_multi_workgroup_plan(dev, T, k, E):
     ids, w = route_topk(logits, k)
     a = fused_moe_packed(x, q1, q2, ids, w)
     assert torch.equal(a, fused_moe_packed(x, q1, q2, ids, w, general_kernel=True))
-    assert torch.equal(a, fused_moe_packed(x, q1, q2, ids, w, wide_kernel=True))
+    assert torch.equal(a, fused_moe_packed(x, q1, q2, ids, w, stream_kernel=True))
     assert_close(a, oracle_out(x, q1, q2, ids, w))
 
 
@@ -270,6 +273,10 @@ def test_wide_kernel_flag_errors(dev):
     w = torch.ones(8, 1, device=dev)
     with pytest.raises(ValueError, match="exclude each other"):
         fused_moe_packed(x, q1, q2, ids, w, wide_kernel=True, general_kernel=True)
+    with pytest.raises(ValueError, match="exclude each other"):
+        fused_moe_packed(x, q1, q2, ids, w, wide_kernel=True, stream_kernel=True)
+    with pytest.raises(NotImplementedError, match="streaming kernels need"):  # hidden 256 is no whole 512 step
+        fused_moe_packed(x, q1, q2, ids, w, stream_kernel=True)
     with pytest.raises(NotImplementedError, match="wide kernels need"):
         fused_moe_packed(x, q1, q2, ids, w, wide_kernel=True, folded_scales=True)
     q1, q2 = make_layer(dev, 4, 128, 64, 4, group=64)  # hidden 128 is not a whole wide item
@@ -285,7 +292,7 @@ def test_streaming_one_hot_expert_many_blocks(dev):
     x = torch.randn(T, 512, generator=g).to(torch.bfloat16).to(dev)
     ids = torch.full((T, 1), 3, dtype=torch.int32, device=dev)
     w = torch.rand(T, 1, generator=g).to(dev)
-    out = fused_moe_packed(x, q1, q2, ids, w)
+    out = fused_moe_packed(x, q1, q2, ids, w, stream_kernel=True)
     assert torch.equal(out, fused_moe_packed(x, q1, q2, ids, w, general_kernel=True))
     assert_close(out, oracle_out(x, q1, q2, ids, w))
 
@@ -301,15 +308,17 @@ def test_streaming_many_experts(dev, E, T, k):
     x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
     logits = torch.randn(T, E, generator=g).to(dev)
     ids, w = route_topk(logits, k)
-    a = fused_moe_packed(x, q1, q2, ids, w)
+    a = fused_moe_packed(x, q1, q2, ids, w, stream_kernel=True)
     assert torch.equal(a, fused_moe_packed(x, q1, q2, ids, w, general_kernel=True))
+    assert torch.equal(a, fused_moe_packed(x, q1, q2, ids, w))
     assert_close(a, oracle_out(x, q1, q2, ids, w))
 
 
 @pytest.mark.parametrize("T,k", [(64, 8), (600, 8)])
 def test_moe_layer_front_end_matches_router_then_forward(dev, T, k):
-    """moe_layer on a streaming shape: T*k <= 2048 lets the GEMMs plan their own
-    blocks, larger T runs the plan kernel; both equal route_topk + fused_moe_packed."""
+    """moe_layer: at T*k <= 2048 (8 rows per expert) the streaming GEMMs plan their own
+    blocks; T=600 (150 rows per expert) runs the plan kernel and the wide GEMMs; both
+    equal route_topk + fused_moe_packed."""
     E, H, I = 32, 1024, 512
     q1, q2 = make_layer(dev, E, H, I, 4, seed=T)
     g = torch.Generator().manual_seed(T + 1)
