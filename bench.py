@@ -58,7 +58,8 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--config", choices=sorted(CONFIGS), default="c4")
+    p.add_argument("--config", choices=sorted(CONFIGS) + ["c5"], default="c4")
+    p.add_argument("--layers", type=int, default=16, help="c5: layers in the stack")
     p.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0: enough to exceed 3x the MALL)")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="bound on the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -285,6 +286,109 @@ def cpu_baseline(torch, cfg, layers, x, logits, budget_s):
             "seconds": round(dt, 2)}
 
 
+def bench_c5(args, torch):
+    """C5: a 16-layer INT4 MoE stack (E64, H2048, I1024, top-8) over 32 x 1024 tokens, timed
+    end to end together with the GPU quantize+pack (MSE scale search, 16 clip ratios in
+    [0.5, 1.0], group 128) of every layer's BF16 weights.  Each layer is
+    h <- h + moe_layer(h) (a residual keeps the activations at unit scale through the
+    stack; the add is inside the timed region).  Layers run as two token chunks of 16384
+    (one library call addresses T*k*H*4 < 2^31 bytes)."""
+    from llada_quant_amd.algorithms.symmetric import quantize_tensor
+    from llada_quant_amd.runtime.fused_moe import _chunks, max_tokens_per_call, moe_layer
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import oracle as O
+
+    E, H, I, k = 64, 2048, 1024, 8
+    L = args.layers
+    T = args.tokens or 32768
+    steps, warmup = max(1, min(args.steps, 5)), min(args.warmup, 1)
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    w1s, w2s, logits = [], [], []
+    for layer in range(L):
+        g = torch.Generator(device=dev).manual_seed(args.seed * 1000 + layer)
+        w1s.append((torch.randn(E, 2 * I, H, generator=g, device=dev) * 0.02).to(torch.bfloat16))
+        w2s.append((torch.randn(E, H, I, generator=g, device=dev) * 0.02).to(torch.bfloat16))
+        logits.append(torch.randn(T, E, generator=g, device=dev))
+    g = torch.Generator(device=dev).manual_seed(args.seed + 7)
+    x = torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16)
+
+    def quantize_all():
+        return [(quantize_tensor(w1, bits=4, group_size=128, scale_search="mse", search_grid=16),
+                 quantize_tensor(w2, bits=4, group_size=128, scale_search="mse", search_grid=16))
+                for w1, w2 in zip(w1s, w2s)]
+
+    def stack(layers):
+        h = x
+        for (q1, q2), lg in zip(layers, logits):
+            out, _ = moe_layer(h, lg, q1, q2, top_k=k)
+            h = h + out
+        return h
+
+    for _ in range(warmup):
+        stack(quantize_all())
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record()
+        layers = quantize_all()
+        ev[i][1].record()
+        h = stack(layers)
+        ev[i][2].record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    quant_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / steps
+    stack_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / steps
+    total_ms = quant_ms + stack_ms
+    # the GPU quantizer against the oracle's restatement of the reference quantizer,
+    # bit for bit, on a sample of rows of layer 0 (w2: 128 rows, w1: 16 rows)
+    exact = True
+    for w, q, rows in ((w2s[0], layers[0][1], 128), (w1s[0], layers[0][0], 16)):
+        wr = w.reshape(-1, w.shape[-1])[:rows].contiguous().cpu()
+        oq, os_, _ = O.quantize(wr.view(torch.int16).numpy().view("uint16"), bits=4, group_size=128,
+                                scale_search="mse", grid=16, w_dtype=O.BF16)
+        gq = q.q.reshape(-1, q.q.shape[-1])[:rows].cpu().numpy()
+        gs = q.scale.reshape(-1, q.scale.shape[-1])[:rows].cpu().numpy()
+        exact = exact and bool((gq == oq).all() and (gs == os_).all())
+    flops = L * 2.0 * T * k * 3 * I * H
+    weights_bf16 = L * E * 3 * I * H * 2
+    packed = L * E * 3 * I * H // 2 + L * E * 3 * I * (H // 128) * 4  # codes + scales (w1: 2I x H/128, w2: H x I/128)
+    stack_tflops = flops / (stack_ms / 1e3) / 1e12
+    result = {
+        "metric": "MoE-layer tokens/s W4A16 64E top-8 H2048; % HBM/MFMA roofline",
+        "value": round(T / (total_ms / 1e3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(total_ms, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {
+            "workload": f"C5: {L}-layer INT4 MoE stack (64 experts, hidden 2048, intermediate 1024, top-8, "
+                        f"residual add) over {T} tokens, timed with the GPU MSE quantize+pack (grid 16) of all layers",
+            "experts": E, "hidden": H, "intermediate": I, "top_k": k, "tokens": T, "layers": L, "bits": 4,
+            "group_size": 128, "calls_per_layer": len(_chunks(T, max_tokens_per_call(H, I, k))),
+            "quantize_ms": round(quant_ms, 3), "stack_ms": round(stack_ms, 3),
+            "layer_ms": round(stack_ms / L, 4), "wall_ms_per_step": round(wall * 1e3, 3),
+            "quantizer": {"bf16_bytes_read": weights_bf16, "packed_bytes_written": packed,
+                          "gbps": round((weights_bf16 + packed) / (quant_ms / 1e3) / 1e9, 1),
+                          "sampled_rows_bitexact_vs_oracle": exact},
+        },
+        "roofline": {"kernel": "MoE stack (wide GEMMs), all layers", "bound": "mfma",
+                     "achieved": round(stack_tflops, 1), "peak": MI355X_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(stack_tflops / MI355X_BF16_TFLOPS, 4), "traffic": None,
+                     "algorithmic_flops": flops, "avg_ms": round(stack_ms, 3)},
+    }
+    if not args.no_cpu:
+        cfg = dict(experts=E, hidden=H, inter=I, top_k=k, tokens=256, bits=4, renorm=False, name="C5 sample")
+        base = cpu_baseline(torch, cfg, layers[:1], x[:256], logits[0][:256], args.cpu_seconds)
+        per_layer = base["value"]
+        base["value"] = round(per_layer / L, 2)
+        base["sample"] = (f"projection: one layer on 256 tokens ({base['sample']}) at {per_layer} tokens/s, "
+                          f"divided by {L} layers; quantizer not included")
+        result["cpu_baseline"] = base
+    del h
+    print(json.dumps(result), flush=True)
+
+
 def main():
     args = parse_args()
     if args.copy_calibration:
@@ -299,6 +403,9 @@ def main():
 
     import torch
 
+    if args.config == "c5":
+        bench_c5(args, torch)
+        return
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from llada_quant_amd.runtime import _lib
     from llada_quant_amd.runtime.fused_moe import _check_weights, workspace_bytes

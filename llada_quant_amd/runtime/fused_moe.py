@@ -85,23 +85,45 @@ def fused_moe_packed(
     device = _lib.require_hip(xc, ids, wts, q1, s1, q2, s2)
     if out is None:
         out = torch.empty(T, H, dtype=torch.bfloat16, device=device)
-    ws_need = workspace_bytes(T, H, I, E, k)
+    spans = _chunks(T, max_tokens_per_call(H, I, k))
+    tc = max(c1 - c0 for c0, c1 in spans)
+    ws_need = workspace_bytes(tc, H, I, E, k)
     if workspace is None or workspace.numel() < ws_need:
         workspace = torch.empty(max(ws_need, 1), dtype=torch.uint8, device=device)
+    flags = (_moe_flags(folded_scales)
+             | (_lib.LQ_MOE_GENERAL_KERNEL if general_kernel else 0)
+             | (_lib.LQ_MOE_WIDE_KERNEL if wide_kernel else 0)
+             | (_lib.LQ_MOE_STREAM_KERNEL if stream_kernel else 0))
     if T:
         lib = _lib.load()
         with torch.cuda.device(device):
-            rc = lib.lq_moe_forward(
-                _lib.ptr(xc), T, H, I, E, k, _lib.ptr(q1), _lib.ptr(s1), _lib.ptr(q2), _lib.ptr(s2), w1.bits, g1, g2,
-                _moe_flags(folded_scales)
-                | (_lib.LQ_MOE_GENERAL_KERNEL if general_kernel else 0)
-                | (_lib.LQ_MOE_WIDE_KERNEL if wide_kernel else 0)
-                | (_lib.LQ_MOE_STREAM_KERNEL if stream_kernel else 0),
-                _lib.ptr(ids), _lib.ptr(wts), _lib.ptr(workspace), workspace.numel(),
-                _lib.ptr(out), _lib.stream(device),
-            )
-        _lib.check(rc, "fused_moe")
+            for c0, c1 in spans:
+                rc = lib.lq_moe_forward(
+                    _lib.ptr(xc[c0:c1]), c1 - c0, H, I, E, k, _lib.ptr(q1), _lib.ptr(s1), _lib.ptr(q2), _lib.ptr(s2),
+                    w1.bits, g1, g2, flags, _lib.ptr(ids[c0:c1]), _lib.ptr(wts[c0:c1]), _lib.ptr(workspace),
+                    workspace.numel(), _lib.ptr(out[c0:c1]), _lib.stream(device),
+                )
+                _lib.check(rc, "fused_moe")
     return out
+
+
+def max_tokens_per_call(H: int, I: int, top_k: int) -> int:
+    """Largest token count one library call takes.
+
+    The kernels address the per-assignment buffers and x with 32-bit buffer
+    offsets: T*k*max(H, I)*4 must stay below 2^31, T*H*2 below the buffer
+    descriptor range, and T <= 2^18.  Larger inputs are split into token
+    chunks by fused_moe_packed and moe_layer (a token's output depends only
+    on its own row and routing, so the split is exact).
+    """
+    lim = min((2**31 - 1) // (top_k * max(H, I) * 4), (0x7FFFFFF0 - 1) // (H * 2), 1 << 18)
+    return max(lim, 1)
+
+
+def _chunks(T: int, lim: int):
+    """Even token ranges [c0, c1) of at most lim tokens covering [0, T)."""
+    n = max(1, -(-T // lim))
+    return [(i * T // n, (i + 1) * T // n) for i in range(n)]
 
 
 def _moe_flags(folded_scales: bool) -> int:
@@ -219,14 +241,19 @@ def moe_layer(
     device = _lib.require_hip(xc, logits, q1c, s1, q2c, s2)
     out = torch.empty(T, H, dtype=torch.bfloat16, device=device)
     ids = torch.empty(T, top_k, dtype=torch.int32, device=device)
-    workspace = torch.empty(max(workspace_bytes(T, H, I, E, top_k), 1), dtype=torch.uint8, device=device)
+    spans = _chunks(T, max_tokens_per_call(H, I, top_k))
+    tc = max(c1 - c0 for c0, c1 in spans)
+    workspace = torch.empty(max(workspace_bytes(tc, H, I, E, top_k), 1), dtype=torch.uint8, device=device)
     if T:
         lib = _lib.load()
+        code = _lib.dtype_code(logits.dtype, "router_logits")
         with torch.cuda.device(device):
-            rc = lib.lq_moe_layer(
-                _lib.ptr(xc), _lib.ptr(logits), _lib.dtype_code(logits.dtype, "router_logits"), T, H, I, E, top_k,
-                int(renormalize), _lib.ptr(q1c), _lib.ptr(s1), _lib.ptr(q2c), _lib.ptr(s2), q1.bits, g1, g2,
-                _moe_flags(folded_scales), _lib.ptr(workspace), workspace.numel(), _lib.ptr(out), _lib.ptr(ids), _lib.stream(device),
-            )
-        _lib.check(rc, "moe_layer")
+            for c0, c1 in spans:
+                rc = lib.lq_moe_layer(
+                    _lib.ptr(xc[c0:c1]), _lib.ptr(logits[c0:c1]), code, c1 - c0, H, I, E, top_k, int(renormalize),
+                    _lib.ptr(q1c), _lib.ptr(s1), _lib.ptr(q2c), _lib.ptr(s2), q1.bits, g1, g2,
+                    _moe_flags(folded_scales), _lib.ptr(workspace), workspace.numel(), _lib.ptr(out[c0:c1]),
+                    _lib.ptr(ids[c0:c1]), _lib.stream(device),
+                )
+                _lib.check(rc, "moe_layer")
     return out.reshape(hidden_states.shape), ids

@@ -167,3 +167,20 @@ def test_int4_layout_validation_runs_on_the_host():
         quantize_tensor(torch.randn(4, 7), bits=4, group_size=-1)
     with pytest.raises(ValueError, match="even group_size"):
         quantize_tensor(torch.randn(4, 96), bits=4, group_size=3)
+
+
+def test_token_chunks_cover_calls_within_the_32bit_bounds():
+    """Layers above one call's addressing bound (T*k*max(H, I)*4 < 2^31) are split into
+    even token chunks: C5's 32768 tokens at top-8, H 2048 become two calls of 16384."""
+    from llada_quant_amd.runtime.fused_moe import _chunks, max_tokens_per_call
+
+    lim = max_tokens_per_call(2048, 1024, 8)
+    assert lim == (2**31 - 1) // (8 * 2048 * 4) == 32767
+    assert _chunks(32768, lim) == [(0, 16384), (16384, 32768)]
+    for T, lim in [(1, 5), (10, 3), (17, 17), (18, 17), (1000, 7)]:
+        spans = _chunks(T, lim)
+        assert spans[0][0] == 0 and spans[-1][1] == T
+        assert all(a1 == b0 for (_, a1), (b0, _) in zip(spans, spans[1:]))
+        assert all(0 < c1 - c0 <= lim for c0, c1 in spans)
+        assert max(c1 - c0 for c0, c1 in spans) - min(c1 - c0 for c0, c1 in spans) <= 1
+    assert max_tokens_per_call(64, 64, 1) == 1 << 18

@@ -266,6 +266,27 @@ def test_multi_workgroup_plan(dev, T, k, E):
     assert_close(a, oracle_out(x, q1, q2, ids, w))
 
 
+def test_token_chunked_calls_match_one_call(dev, monkeypatch):
+    """Calls above one call's addressing bound are split into token chunks; with the
+    bound lowered to 37 tokens, chunked moe_layer and fused_moe_packed give the bits
+    of one whole call (each token's output depends only on its own row and routing)."""
+    from llada_quant_amd.runtime import fused_moe as FM
+
+    E, H, I, T, k = 16, 512, 512, 150, 4
+    q1, q2 = make_layer(dev, E, H, I, 4, seed=31)
+    g = torch.Generator().manual_seed(31)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    logits = torch.randn(T, E, generator=g).to(dev)
+    out, ids = moe_layer(x, logits, q1, q2, top_k=k)
+    ids2, w2 = route_topk(logits, k)
+    whole = fused_moe_packed(x, q1, q2, ids2, w2)
+    monkeypatch.setattr(FM, "max_tokens_per_call", lambda H, I, top_k: 37)
+    out_c, ids_c = moe_layer(x, logits, q1, q2, top_k=k)
+    assert torch.equal(ids, ids_c) and torch.equal(out, out_c)
+    assert torch.equal(whole, fused_moe_packed(x, q1, q2, ids2, w2))
+    assert torch.equal(out, whole)
+
+
 def test_wide_kernel_flag_errors(dev):
     q1, q2 = make_layer(dev, 4, 256, 128, 4)
     x = torch.randn(8, 256, device=dev).to(torch.bfloat16)
