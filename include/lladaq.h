@@ -229,6 +229,28 @@ int lq_moe_layer(const void *x, const void *logits, int logits_dtype,
  */
 int lq_moe_profile_events(void *const *events, int n_events);
 
+/*
+ * QuantLinear forward (replaces runtime/linear.py:127-131, QuantLinear.forward
+ * = F.linear(x.to(bf16), dequantize_weight()), with the dequantize of
+ * runtime/linear.py:103-111 fused into the GEMM):
+ *   out [M, N] bf16 = bf16(x [M, K] bf16 . W^T), fp32 accumulation, where
+ *   W = bf16(fp32(q) * s) is the reference's dequantized weight bit for bit;
+ *   q [N, K] int8 or [N, K/2] packed INT4, s [N, K/G] f32 (group = -1 or
+ *   K % group != 0: one group per row).
+ * Requires N % 128 == 0, K % 64 == 0, group length % 32 == 0, M <= 262144.
+ * flags: 0, LQ_MOE_WIDE_KERNEL or LQ_MOE_GENERAL_KERNEL (same results).  The
+ * bias of the reference module is added by the caller (a bf16 add after the
+ * bf16 product, as the reference does).  Kernels on `stream`: set-up, plan,
+ * GEMM, combine; no host synchronisation, no device allocation.
+ */
+int lq_quant_linear(const void *x, int64_t M, int K, int N, const int8_t *q,
+                    const float *s, int bits, int64_t group, int flags,
+                    void *workspace, size_t ws_bytes, void *out,
+                    lq_stream_t stream);
+
+/* Bytes of workspace lq_quant_linear needs for M rows, K in, N out features. */
+size_t lq_linear_workspace_bytes(int64_t M, int K, int N);
+
 #ifdef __cplusplus
 }
 #endif

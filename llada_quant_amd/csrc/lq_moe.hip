@@ -1813,6 +1813,19 @@ __global__ __launch_bounds__(256) void permute_rows_kernel(const uint16_t *__res
     reinterpret_cast<uint4 *>(xperm)[i] = permute_kslots(reinterpret_cast<const uint4 *>(x)[i]);
 }
 
+// QuantLinear set-up: x [M, K] -> act [M, K] in the GEMMs' K-slot order
+// (8 values per thread), every row routed to expert 0 with weight 1.0
+__global__ __launch_bounds__(256) void linear_setup_kernel(const uint16_t *__restrict__ x, int64_t n8, int64_t M,
+                                                           uint16_t *__restrict__ act, int32_t *__restrict__ ids,
+                                                           float *__restrict__ weights) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n8) reinterpret_cast<uint4 *>(act)[i] = permute_kslots(reinterpret_cast<const uint4 *>(x)[i]);
+  if (i < M) {
+    ids[i] = 0;
+    weights[i] = 1.0f;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
@@ -2346,4 +2359,121 @@ extern "C" int lq_moe_layer(const void *x, const void *logits, int logits_dtype,
   pm.mark(1);
   return moe_forward_impl(x, true, T, H, I, E, k, q1, s1, q2, s2, bits, group_w1, group_w2, flags, ids,
                           weights, ws, out, st, pm, 2);
+}
+
+// QuantLinear (runtime/linear.py:127-131): out = bf16(x . dequant(W)^T) with
+// fp32 accumulation, W [N, K] packed INT4 / INT8 with fp32 group scales
+// along K -- the layer's second GEMM with one expert, top-1, weight 1.0:
+// set-up (x into K-slot order, ids 0, weights 1), plan, GEMM2 (wide at
+// >= 32 rows when N % 256 == 0 and K % 256 == 0, else general), combine.
+extern "C" size_t lq_linear_workspace_bytes(int64_t M, int K, int N) {
+  if (M < 0 || K <= 0 || N <= 0) return 0;
+  return ws_layout(M, N, K, 1, 1).total;
+}
+
+extern "C" int lq_quant_linear(const void *x, int64_t M, int K, int N, const int8_t *q, const float *s, int bits,
+                               int64_t group, int flags, void *workspace, size_t ws_bytes, void *out,
+                               lq_stream_t stream) {
+  const hipStream_t st = as_stream(stream);
+  if (bits != 4 && bits != 8) return fail(LQ_ERR_VALUE, "bits must be 8 or 4, got " + std::to_string(bits));
+  if (M < 0 || K <= 0 || N <= 0) return fail(LQ_ERR_VALUE, "quant_linear: bad shape");
+  if (flags & ~(LQ_MOE_GENERAL_KERNEL | LQ_MOE_WIDE_KERNEL)) return fail(LQ_ERR_VALUE, "quant_linear: unknown flags");
+  if ((flags & LQ_MOE_GENERAL_KERNEL) && (flags & LQ_MOE_WIDE_KERNEL))
+    return fail(LQ_ERR_VALUE, "quant_linear: LQ_MOE_WIDE_KERNEL and LQ_MOE_GENERAL_KERNEL exclude each other");
+  if (N % kR2 != 0 || K % kF1 != 0)
+    return fail(LQ_ERR_UNSUPPORTED, "quant_linear: needs out_features % 128 == 0 and in_features % 64 == 0");
+  const int64_t g = effective_group(K, group);
+  if (g % 32 != 0)
+    return fail(LQ_ERR_UNSUPPORTED, "quant_linear: the group length along K must be a multiple of 32 (got " +
+                                        std::to_string(g) + ")");
+  const bool wide_ok = wide_eligible(N, K, 0);
+  if ((flags & LQ_MOE_WIDE_KERNEL) && !wide_ok)
+    return fail(LQ_ERR_UNSUPPORTED, "quant_linear: the wide kernels need out_features % 256 == 0 and "
+                                    "in_features % 256 == 0");
+  if (M > (int64_t{1} << 18) || M * static_cast<int64_t>(N > K ? N : K) * 4 > 0x7FFFFFFFll ||
+      M * static_cast<int64_t>(K) * 2 >= kOutOfRange)
+    return fail(LQ_ERR_UNSUPPORTED, "quant_linear: too many rows for one call");
+  if (int64_t{1} * N * K >= kOutOfRange) return fail(LQ_ERR_UNSUPPORTED, "quant_linear: weight exceeds 2 GiB");
+  if (M == 0) return LQ_OK;
+  if (!x || !q || !s || !workspace || !out) return fail(LQ_ERR_VALUE, "quant_linear: null pointer");
+  if (!aligned16(x) || !aligned16(q) || !aligned16(workspace) || !aligned16(out))
+    return fail(LQ_ERR_VALUE, "quant_linear: x, qweight, workspace and out must be 16-byte aligned");
+  const WsLayout w = ws_layout(M, N, K, 1, 1);
+  if (ws_bytes < w.total)
+    return fail(LQ_ERR_VALUE, "quant_linear: workspace too small (" + std::to_string(ws_bytes) + " < " +
+                                  std::to_string(w.total) + ")");
+  char *ws = static_cast<char *>(workspace);
+  const bool wide = (flags & LQ_MOE_WIDE_KERNEL) || (!(flags & LQ_MOE_GENERAL_KERNEL) && wide_ok && M >= kWideMinRows);
+  int32_t *ids = reinterpret_cast<int32_t *>(ws + w.ids);
+  float *weights = reinterpret_cast<float *>(ws + w.weights);
+  uint16_t *act = reinterpret_cast<uint16_t *>(ws + w.act);
+  const int64_t n8 = M * K / 8;
+  linear_setup_kernel<<<static_cast<int>(ceil_div(std::max(n8, M), 256)), 256, 0, st>>>(
+      static_cast<const uint16_t *>(x), n8, M, act, ids, weights);
+  int rc = check_launch("quant_linear_setup");
+  if (rc) return rc;
+  PlanArgs p = plan_args(ids, M, 1, 1, ws, w);
+  p.block_rows = wide ? kWRows : kRowsMax;
+  const int64_t nseg = ceil_div(M, kPlanSeg);
+  if (nseg > 1) {
+    int32_t *segcnt = reinterpret_cast<int32_t *>(ws + w.segcnt);
+    plan_count_kernel<<<static_cast<int>(nseg), kPlanBlock, 0, st>>>(p, segcnt);
+    rc = check_launch("quant_linear_plan_count");
+    if (rc) return rc;
+    plan_scatter_kernel<<<static_cast<int>(nseg), kPlanBlock, 0, st>>>(p, segcnt, static_cast<int>(nseg));
+  } else {
+    plan_kernel<<<1, kPlanBlock, 0, st>>>(p);
+  }
+  rc = check_launch("quant_linear_plan");
+  if (rc) return rc;
+  MoeArgs a{};
+  a.q2 = q;
+  a.s2 = s;
+  a.ids = ids;
+  a.topk_w = weights;
+  a.offsets = p.offsets;
+  a.sorted = p.sorted;
+  a.blocks = p.blocks;
+  a.srow = p.srow;
+  a.hdr = p.hdr;
+  a.act = act;
+  a.ybuf = reinterpret_cast<float *>(ws + w.ybuf);
+  a.out = static_cast<uint16_t *>(out);
+  a.T = M;
+  a.H = N;
+  a.I = K;
+  a.E = 1;
+  a.k = 1;
+  a.g2 = static_cast<int>(g);
+  a.ng2 = static_cast<int>(K / g);
+  const int64_t blocks = max_blocks_for(M, 1, 1);
+  if (wide) {
+    const int64_t items = (1 + M / kWRows) * (N / kWR2);
+    const bool g128 = a.g2 == kKC;
+    if (bits == 4 && g128)
+      moe_wide_kernel<4, false, true><<<wide_grid<4, false, true>(items), kWThreads, 0, st>>>(a);
+    else if (bits == 4)
+      moe_wide_kernel<4, false, false><<<wide_grid<4, false, false>(items), kWThreads, 0, st>>>(a);
+    else if (g128)
+      moe_wide_kernel<8, false, true><<<wide_grid<8, false, true>(items), kWThreads, 0, st>>>(a);
+    else
+      moe_wide_kernel<8, false, false><<<wide_grid<8, false, false>(items), kWThreads, 0, st>>>(a);
+  } else {
+    const int64_t items = blocks * (N / kR2);
+    const bool g128 = a.g2 == kKC;
+    if (bits == 4 && g128)
+      moe_gemm_kernel<4, false, false, true><<<gemm_grid<4, false, false, true>(items), kThreads, 0, st>>>(a);
+    else if (bits == 4)
+      moe_gemm_kernel<4, false, false, false><<<gemm_grid<4, false, false, false>(items), kThreads, 0, st>>>(a);
+    else if (g128)
+      moe_gemm_kernel<8, false, false, true><<<gemm_grid<8, false, false, true>(items), kThreads, 0, st>>>(a);
+    else
+      moe_gemm_kernel<8, false, false, false><<<gemm_grid<8, false, false, false>(items), kThreads, 0, st>>>(a);
+  }
+  rc = check_launch("quant_linear_gemm");
+  if (rc) return rc;
+  const int64_t n2 = M * N / 2;
+  combine_kernel<<<static_cast<int>(ceil_div(n2, kCombineBlock)), kCombineBlock, 0, st>>>(a.ybuf, ids, M, N, 1, 1,
+                                                                                          a.out);
+  return check_launch("quant_linear_combine");
 }

@@ -50,6 +50,8 @@ SIGNATURES = {
     "lq_moe_layer": (_I32, [_P, _P, _I32, _I64, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _I32, _I64, _I64,
                             _I32, _P, _SZ, _P, _P, _P]),
     "lq_moe_profile_events": (_I32, [_P, _I32]),
+    "lq_quant_linear": (_I32, [_P, _I64, _I32, _I32, _P, _P, _I32, _I64, _I32, _P, _SZ, _P, _P]),
+    "lq_linear_workspace_bytes": (_SZ, [_I64, _I32, _I32]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
