@@ -58,7 +58,7 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--config", choices=sorted(CONFIGS) + ["c5"], default="c4")
+    p.add_argument("--config", choices=sorted(CONFIGS) + ["c5", "linear"], default="c4")
     p.add_argument("--layers", type=int, default=16, help="c5: layers in the stack")
     p.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0: enough to exceed 3x the MALL)")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="bound on the CPU baseline sample")
@@ -286,6 +286,64 @@ def cpu_baseline(torch, cfg, layers, x, logits, budget_s):
             "seconds": round(dt, 2)}
 
 
+def bench_linear(args, torch):
+    """QuantLinear (W8A16, group 128) on the reference's own benchmark shape: a 64 MiB weight
+    (8192 x 8192 INT8), M = 16 / 64 / 128 / 256 rows (runtime/kernels/w8a16_gemm.py:1-11),
+    against torch's BF16 GEMM on the already-dequantized weight on the same GPU.  Six weight
+    copies (384 MiB of codes) rotate so the codes stream from HBM."""
+    from llada_quant_amd.algorithms.symmetric import quantize_tensor
+    from llada_quant_amd.runtime.linear import quant_linear
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    N = K = 8192
+    copies = 6
+    qs, wd = [], []
+    for c in range(copies):
+        g = torch.Generator(device=dev).manual_seed(args.seed * 100 + c)
+        w = (torch.randn(N, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        q = quantize_tensor(w, bits=8, group_size=128)
+        qs.append(q)
+        wd.append(q.dequantize(torch.bfloat16).t().contiguous())  # [K, N] for x @ w
+        del w
+    steps = max(10, min(args.steps, 200))
+    rows = []
+    for M in (16, 64, 128, 256):
+        x = torch.randn(M, K, device=dev).to(torch.bfloat16)
+
+        def timed(fn):
+            for i in range(3):
+                fn(i)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            a.record()
+            for i in range(steps):
+                fn(i)
+            b.record()
+            torch.cuda.synchronize()
+            return a.elapsed_time(b) / steps
+
+        ms = timed(lambda i: quant_linear(x, qs[i % copies].q, qs[i % copies].scale, 8, 128))
+        ms_bf16 = timed(lambda i: x @ wd[i % copies])
+        algo = N * K + N * (K // 128) * 4 + M * K * 2 + M * N * 2
+        rows.append({"M": M, "ms": round(ms, 5), "gbps": round(algo / (ms / 1e3) / 1e9, 1),
+                     "hbm_frac": round(algo / (ms / 1e3) / 1e9 / MI355X_HBM_GBPS, 4),
+                     "bf16_dequantized_ms": round(ms_bf16, 5), "speedup_vs_bf16": round(ms_bf16 / ms, 3)})
+    r0 = rows[0]
+    result = {
+        "metric": "QuantLinear W8A16 rows/s, 64 MiB weight; % HBM roofline",
+        "value": round(16 / (r0["ms"] / 1e3), 1), "unit": "rows/s", "n_gpus": 1, "steps": steps, "warmup": 3,
+        "ms_per_step": r0["ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "QuantLinear W8A16: x [M, 8192] bf16 . W^T, W 8192 x 8192 INT8 g128 amax, M = 16",
+                   "sweep": rows},
+        "roofline": {"kernel": "lq_quant_linear at M = 16 (general GEMM2, one expert)", "bound": "hbm",
+                     "achieved": r0["gbps"], "peak": MI355X_HBM_GBPS, "unit": "GB/s", "frac": r0["hbm_frac"],
+                     "traffic": None, "avg_ms": r0["ms"]},
+    }
+    print(json.dumps(result), flush=True)
+
+
 def bench_c5(args, torch):
     """C5: a 16-layer INT4 MoE stack (E64, H2048, I1024, top-8) over 32 x 1024 tokens, timed
     end to end together with the GPU quantize+pack (MSE scale search, 16 clip ratios in
@@ -405,6 +463,9 @@ def main():
 
     if args.config == "c5":
         bench_c5(args, torch)
+        return
+    if args.config == "linear":
+        bench_linear(args, torch)
         return
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from llada_quant_amd.runtime import _lib

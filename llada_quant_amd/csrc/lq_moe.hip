@@ -104,6 +104,7 @@ struct MoeArgs {
   int64_t T;
   int H, I, E, k;
   int g1, ng1, g2, ng2;    // group length and groups per row of w1 / w2
+  int ksplit;              // general G2 only: K slices per item (partial sums to ybuf slot asg * ksplit + ks)
 };
 
 // ---------------------------------------------------------------------------
@@ -292,7 +293,7 @@ __device__ __forceinline__ void chunk_mfma(const WChunk<BITS> (&w)[NT], const fl
 // ---------------------------------------------------------------------------
 
 template <int BITS, bool FOLDED, int NRT, bool FIRST, bool G128>
-__device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, int row0, int rows,
+__device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, int row0, int rows, int ks,
                                           unsigned char *lds) {
   constexpr int kD = depth_for<BITS>();
   static_assert(kD == 2 || kD == 4, "the K loop is unrolled for depth 2 or 4");
@@ -302,7 +303,11 @@ __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, in
   const int lc = lane & 15;
   const int lg = lane >> 4;
   const int K = FIRST ? a.H : a.I;
-  const int nk = (K + kKC - 1) / kKC;
+  // split K (G2, ksplit > 1, K / ksplit a multiple of 128): this item sums
+  // chunks [c0, c0 + nk) of the full K; chunk i below is chunk c0 + i
+  const int ksplit = FIRST ? 1 : a.ksplit;
+  const int nk = ksplit > 1 ? K / kKC / ksplit : (K + kKC - 1) / kKC;
+  const int c0 = ks * nk;
 
   // ---- token rows (all four waves stage them): a chunk is NRT*16 rows x 16
   // pieces of 16 bytes; wave w, lane l owns pieces w*64 + l + 256q (q < NRT):
@@ -317,7 +322,7 @@ __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, in
   // compiler counts the loads in flight exactly) and never reads outside its
   // operands.  Only the partial last chunk of a K that is not a multiple of
   // 128 takes per-lane offsets (ktail).
-  const bool ktail = (K % kKC) != 0;
+  const bool ktail = ksplit == 1 && (K % kKC) != 0;
   const __amdgpu_buffer_rsrc_t arsrc = make_rsrc(FIRST ? static_cast<const void *>(a.xperm) : a.act,
                                                  FIRST ? a.T * a.H * 2 : a.T * a.k * a.I * 2);
   int avoff[NRT];    // byte offset of each owned row piece in chunk 0 (row 0 for padding rows)
@@ -340,7 +345,7 @@ __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, in
     const bool tail = ktail && i == nk - 1;
 #pragma unroll
     for (int q = 0; q < NRT; ++q)
-      v[q] = __builtin_amdgcn_raw_buffer_load_b128(r, tail ? avoff_t[q] : avoff[q], i * kKC * 2, 0);
+      v[q] = __builtin_amdgcn_raw_buffer_load_b128(r, tail ? avoff_t[q] : avoff[q], (c0 + i) * kKC * 2, 0);
   };
   auto store_a = [&](int i, const u32x4(&v)[NRT]) __attribute__((always_inline)) {
     unsigned char *buf = lds + (i % kStages) * kStageBytes;
@@ -386,16 +391,18 @@ __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, in
     for (int c = 0; c < 2; ++c) {
       const int vo = tail ? wvoff_t[c] : wvoff[c];
       if constexpr (BITS == 4) {
-        w[c].v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vo, i * kChunkBytes, 0));
+        w[c].v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vo, (c0 + i) * kChunkBytes, 0));
       } else {
-        w[c].v0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vo, i * kChunkBytes, 0));
-        w[c].v1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vo + 16, i * kChunkBytes, 0));
+        w[c].v0 =
+            __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vo, (c0 + i) * kChunkBytes, 0));
+        w[c].v1 =
+            __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vo + 16, (c0 + i) * kChunkBytes, 0));
       }
       if constexpr (G128) {
-        sc[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, svoff[c], i * 4, 0));
+        sc[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, svoff[c], (c0 + i) * 4, 0));
       } else {
         // group of this lane's K values (FOLDED: of the chunk, G % 128 == 0)
-        const int sidx = (FOLDED ? i * kKC : min(i * kKC + 32 * lg, K - 1)) / G;
+        const int sidx = (FOLDED ? (c0 + i) * kKC : min((c0 + i) * kKC + 32 * lg, K - 1)) / G;
         sc[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, svoff[c] + 4 * sidx, 0, 0));
       }
     }
@@ -499,7 +506,7 @@ __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, in
         if (m < rows) {
           const int asg = a.sorted[row0 + m];
           const float wt = a.topk_w[asg];
-          float *yrow = a.ybuf + static_cast<int64_t>(asg) * a.H;
+          float *yrow = a.ybuf + (static_cast<int64_t>(asg) * ksplit + ks) * a.H;
           yrow[wr[0]] = tot[rt][0][j] * wt;
           yrow[wr[1]] = tot[rt][1][j] * wt;
         }
@@ -508,12 +515,12 @@ __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, in
 }
 
 template <int BITS, bool FOLDED, bool FIRST, bool G128>
-__device__ __forceinline__ void gemm_dispatch(const MoeArgs &a, int e, int slice, int row0, int rows,
+__device__ __forceinline__ void gemm_dispatch(const MoeArgs &a, int e, int slice, int row0, int rows, int ks,
                                               unsigned char *lds) {
   if (rows <= 16)
-    gemm_item<BITS, FOLDED, 1, FIRST, G128>(a, e, slice, row0, rows, lds);
+    gemm_item<BITS, FOLDED, 1, FIRST, G128>(a, e, slice, row0, rows, ks, lds);
   else
-    gemm_item<BITS, FOLDED, 2, FIRST, G128>(a, e, slice, row0, rows, lds);
+    gemm_item<BITS, FOLDED, 2, FIRST, G128>(a, e, slice, row0, rows, ks, lds);
 }
 
 // out[t, h..h+2) = bf16(sum_j y[t*k + j, h..h+2)) over the routed slots, j
@@ -564,7 +571,8 @@ template <int BITS, bool FOLDED, bool FIRST, bool G128>
 __global__ __launch_bounds__(kThreads, 3) void moe_gemm_kernel(MoeArgs a) {
   __shared__ __align__(16) unsigned char lds[kStages * kStageBytes];
   const int nb = __builtin_amdgcn_readfirstlane(a.hdr->n_blk);
-  const int per = FIRST ? a.I / kF1 : a.H / kR2;
+  const int ksplit = FIRST ? 1 : a.ksplit;
+  const int per = (FIRST ? a.I / kF1 : a.H / kR2) * ksplit;  // items per block: slices x K slices
   const int n = nb * per;
   const int xcd = blockIdx.x & 7;
   const int gx = gridDim.x >> 3;
@@ -573,12 +581,14 @@ __global__ __launch_bounds__(kThreads, 3) void moe_gemm_kernel(MoeArgs a) {
   // every value below is wave-uniform (scalar): the item body contains barriers
   for (int t = xcd * n8 + static_cast<int>(blockIdx.x >> 3); t < end; t += gx) {
     const int blk = t / per;
-    const int slice = t - blk * per;
+    const int rem = t - blk * per;
+    const int slice = rem / ksplit;
+    const int ks = rem - slice * ksplit;
     const int4 bi = a.blocks[blk];
     const int e = __builtin_amdgcn_readfirstlane(bi.x);
     const int row0 = __builtin_amdgcn_readfirstlane(bi.y);
     const int rows = __builtin_amdgcn_readfirstlane(bi.z);
-    gemm_dispatch<BITS, FOLDED, FIRST, G128>(a, e, slice, row0, rows, lds);
+    gemm_dispatch<BITS, FOLDED, FIRST, G128>(a, e, slice, row0, rows, ks, lds);
   }
 }
 
@@ -2265,6 +2275,7 @@ int moe_forward_impl(const void *x, bool x_permuted, int64_t T, int H, int I, in
   a.ng1 = static_cast<int>(H / g1);
   a.g2 = static_cast<int>(g2);
   a.ng2 = static_cast<int>(I / g2);
+  a.ksplit = 1;
   const int64_t blocks = max_blocks_for(T, E, k);
   const int64_t max_g1 = blocks * (I / kF1), max_g2 = blocks * (H / kR2);
   if (bits == 4)
@@ -2361,14 +2372,37 @@ extern "C" int lq_moe_layer(const void *x, const void *logits, int logits_dtype,
                           weights, ws, out, st, pm, 2);
 }
 
+// K slices of the general GEMM for QuantLinear: with few row blocks the
+// items (block, 128-row slice) cannot fill the GPU, so each item also takes
+// one of S equal K slices (whole 128-wide chunks) and writes its partial sums
+// to slot S * row + slice of the workspace; the combine adds the S slots in
+// ascending order (deterministic).  S doubles until about 512 items exist
+// (two per CU), capped at 16.  A pure function of the shape, so the
+// workspace query and the call agree.
+int linear_ksplit(int64_t M, int K, int N) {
+  if (K % kKC != 0) return 1;
+  const int64_t items = ceil_div(M, kRowsMax) * (N / kR2);
+  const int nkc = K / kKC;
+  int S = 1;
+  while (items * S < 512 && S < 16 && nkc % (2 * S) == 0) S *= 2;
+  return S;
+}
+
+// the wide kernels take a QuantLinear when their items alone fill the GPU
+bool linear_wide(int64_t M, int K, int N, int flags) {
+  if (flags & LQ_MOE_WIDE_KERNEL) return true;
+  if (flags & LQ_MOE_GENERAL_KERNEL) return false;
+  return wide_eligible(N, K, 0) && M >= kWideMinRows && ceil_div(M, kWRows) * (N / kWR2) >= 256;
+}
+
 // QuantLinear (runtime/linear.py:127-131): out = bf16(x . dequant(W)^T) with
 // fp32 accumulation, W [N, K] packed INT4 / INT8 with fp32 group scales
 // along K -- the layer's second GEMM with one expert, top-1, weight 1.0:
-// set-up (x into K-slot order, ids 0, weights 1), plan, GEMM2 (wide at
-// >= 32 rows when N % 256 == 0 and K % 256 == 0, else general), combine.
+// set-up (x into K-slot order, ids 0, weights 1), plan, GEMM2 (wide when its
+// items fill the GPU, else general with K slices), combine.
 extern "C" size_t lq_linear_workspace_bytes(int64_t M, int K, int N) {
   if (M < 0 || K <= 0 || N <= 0) return 0;
-  return ws_layout(M, N, K, 1, 1).total;
+  return ws_layout(M, N, K, 1, linear_ksplit(M, K, N)).total;
 }
 
 extern "C" int lq_quant_linear(const void *x, int64_t M, int K, int N, const int8_t *q, const float *s, int bits,
@@ -2398,18 +2432,19 @@ extern "C" int lq_quant_linear(const void *x, int64_t M, int K, int N, const int
   if (!x || !q || !s || !workspace || !out) return fail(LQ_ERR_VALUE, "quant_linear: null pointer");
   if (!aligned16(x) || !aligned16(q) || !aligned16(workspace) || !aligned16(out))
     return fail(LQ_ERR_VALUE, "quant_linear: x, qweight, workspace and out must be 16-byte aligned");
-  const WsLayout w = ws_layout(M, N, K, 1, 1);
+  const bool wide = linear_wide(M, K, N, flags);
+  const int S = wide ? 1 : linear_ksplit(M, K, N);
+  const WsLayout w = ws_layout(M, N, K, 1, linear_ksplit(M, K, N));
   if (ws_bytes < w.total)
     return fail(LQ_ERR_VALUE, "quant_linear: workspace too small (" + std::to_string(ws_bytes) + " < " +
                                   std::to_string(w.total) + ")");
   char *ws = static_cast<char *>(workspace);
-  const bool wide = (flags & LQ_MOE_WIDE_KERNEL) || (!(flags & LQ_MOE_GENERAL_KERNEL) && wide_ok && M >= kWideMinRows);
   int32_t *ids = reinterpret_cast<int32_t *>(ws + w.ids);
   float *weights = reinterpret_cast<float *>(ws + w.weights);
   uint16_t *act = reinterpret_cast<uint16_t *>(ws + w.act);
   const int64_t n8 = M * K / 8;
-  linear_setup_kernel<<<static_cast<int>(ceil_div(std::max(n8, M), 256)), 256, 0, st>>>(
-      static_cast<const uint16_t *>(x), n8, M, act, ids, weights);
+  linear_setup_kernel<<<static_cast<int>(ceil_div(std::max(n8, M * S), 256)), 256, 0, st>>>(
+      static_cast<const uint16_t *>(x), n8, M * S, act, ids, weights);
   int rc = check_launch("quant_linear_setup");
   if (rc) return rc;
   PlanArgs p = plan_args(ids, M, 1, 1, ws, w);
@@ -2446,6 +2481,7 @@ extern "C" int lq_quant_linear(const void *x, int64_t M, int K, int N, const int
   a.k = 1;
   a.g2 = static_cast<int>(g);
   a.ng2 = static_cast<int>(K / g);
+  a.ksplit = S;
   const int64_t blocks = max_blocks_for(M, 1, 1);
   if (wide) {
     const int64_t items = (1 + M / kWRows) * (N / kWR2);
@@ -2459,7 +2495,7 @@ extern "C" int lq_quant_linear(const void *x, int64_t M, int K, int N, const int
     else
       moe_wide_kernel<8, false, false><<<wide_grid<8, false, false>(items), kWThreads, 0, st>>>(a);
   } else {
-    const int64_t items = blocks * (N / kR2);
+    const int64_t items = blocks * (N / kR2) * S;
     const bool g128 = a.g2 == kKC;
     if (bits == 4 && g128)
       moe_gemm_kernel<4, false, false, true><<<gemm_grid<4, false, false, true>(items), kThreads, 0, st>>>(a);
@@ -2473,7 +2509,7 @@ extern "C" int lq_quant_linear(const void *x, int64_t M, int K, int N, const int
   rc = check_launch("quant_linear_gemm");
   if (rc) return rc;
   const int64_t n2 = M * N / 2;
-  combine_kernel<<<static_cast<int>(ceil_div(n2, kCombineBlock)), kCombineBlock, 0, st>>>(a.ybuf, ids, M, N, 1, 1,
+  combine_kernel<<<static_cast<int>(ceil_div(n2, kCombineBlock)), kCombineBlock, 0, st>>>(a.ybuf, ids, M, N, S, 1,
                                                                                           a.out);
   return check_launch("quant_linear_combine");
 }

@@ -4,10 +4,11 @@ The reference module computes ``F.linear(x.bf16, dequantize_weight())``
 (runtime/linear.py:127-131).  Its own kernel tests (tests/unit/test_w8a16_kernel.py:33-82)
 hold a packed GEMM to the fp32 truth ``x . dequant(W)^T``: relative L2 error
 below 3e-3 (the bf16 output-rounding floor) and no more than 1.2x that of the
-BLAS product on the same dequantized weight.  The same bars apply here, with
-the dequantized weight taken from the CPU oracle (bit-exact restatement of
-dequantize_tensor), and the wide and general GEMM families must agree bit
-for bit.
+BLAS product on the same dequantized weight.  The same bars apply here, to
+each GEMM family, with the dequantized weight taken from the CPU oracle
+(bit-exact restatement of dequantize_tensor).  With few rows the general
+family splits K into slices whose partial sums the combine adds in order,
+so the families differ in summation order; each call is deterministic.
 """
 
 from __future__ import annotations
@@ -40,6 +41,7 @@ def rel(out: torch.Tensor, truth: torch.Tensor) -> float:
     (129, 2048, 2048, 8, 128),  # test_w8a16_kernel.py's shape at a ragged M
     (300, 1024, 768, 4, 128),
     (16, 512, 256, 8, -1),     # one group per row
+    (2, 8192, 512, 4, 128),    # long K: 16 K slices per item
 ])
 def test_quant_linear_matches_truth_and_blas(dev, M, K, N, bits, group):
     g = torch.Generator().manual_seed(M + K + N)
@@ -52,13 +54,15 @@ def test_quant_linear_matches_truth_and_blas(dev, M, K, N, bits, group):
     out = quant_linear(x, q.q, q.scale, bits, group)
     assert out.shape == (M, N) and out.dtype == torch.bfloat16
     blas = x @ q.dequantize(torch.bfloat16).t().contiguous()  # bf16 BLAS product, contiguous operands
-    err, err_blas = rel(out, truth), rel(blas, truth)
-    assert err < 3e-3, f"relative L2 error {err:.2e}"
-    assert err <= 1.2 * err_blas + 1e-6, f"{err:.2e} against the BLAS product's {err_blas:.2e}"
-    general = quant_linear(x, q.q, q.scale, bits, group, general_kernel=True)
-    assert torch.equal(out, general)
+    err_blas = rel(blas, truth)
+    runs = {"auto": out, "general": quant_linear(x, q.q, q.scale, bits, group, general_kernel=True)}
     if K % 256 == 0 and N % 256 == 0:
-        assert torch.equal(out, quant_linear(x, q.q, q.scale, bits, group, wide_kernel=True))
+        runs["wide"] = quant_linear(x, q.q, q.scale, bits, group, wide_kernel=True)
+    for name, o in runs.items():
+        err = rel(o, truth)
+        assert err < 3e-3, f"{name}: relative L2 error {err:.2e}"
+        assert err <= 1.2 * err_blas + 1e-6, f"{name}: {err:.2e} against the BLAS product's {err_blas:.2e}"
+    assert torch.equal(out, quant_linear(x, q.q, q.scale, bits, group))  # deterministic
 
 
 def test_quant_linear_module_from_linear(dev):
