@@ -248,6 +248,21 @@ int lq_quant_linear(const void *x, int64_t M, int K, int N, const int8_t *q,
                     void *workspace, size_t ws_bytes, void *out,
                     lq_stream_t stream);
 
+/*
+ * Router GEMM fused with the top-k softmax router (trajectory/llada.py:228-234
+ * with the gate in front: router_logits = block.gate(x_flat), a bias-free
+ * bf16 nn.Linear, then softmax(dtype=float32).topk(k)):
+ *   x [T, H] bf16, gate_weight [E, H] bf16 (E <= 64, H % 32 == 0, both
+ *   16-byte aligned); logits = bf16(x . gate_weight^T) with fp32
+ *   accumulation; ids / weights as lq_route_topk computes them from those
+ *   logits; logits_out [T, E] bf16 receives the logits when not NULL (the
+ *   reference's routing hook records them).
+ */
+int lq_route_gemm_topk(const void *x, const void *gate_weight, int64_t T,
+                       int H, int E, int k, int renormalize,
+                       int32_t *topk_ids, float *topk_weights,
+                       void *logits_out, lq_stream_t stream);
+
 /* Bytes of workspace lq_quant_linear needs for M rows, K in, N out features. */
 size_t lq_linear_workspace_bytes(int64_t M, int K, int N);
 

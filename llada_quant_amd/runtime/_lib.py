@@ -52,6 +52,7 @@ SIGNATURES = {
     "lq_moe_profile_events": (_I32, [_P, _I32]),
     "lq_quant_linear": (_I32, [_P, _I64, _I32, _I32, _P, _P, _I32, _I64, _I32, _P, _SZ, _P, _P]),
     "lq_linear_workspace_bytes": (_SZ, [_I64, _I32, _I32]),
+    "lq_route_gemm_topk": (_I32, [_P, _P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

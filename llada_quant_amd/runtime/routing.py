@@ -51,6 +51,39 @@ def route_topk(logits: torch.Tensor, top_k: int, renormalize: bool = False) -> T
     return ids, weights
 
 
+def route_gemm_topk(hidden_states: torch.Tensor, gate_weight: torch.Tensor, top_k: int,
+                    renormalize: bool = False, return_logits: bool = False):
+    """Router GEMM + top-k in one kernel: ``(ids, weights[, logits])`` for ``hidden_states [..., H]``.
+
+    ``logits = bf16(x . gate_weight^T)`` (``block.gate(x_flat)``, a bias-free bf16
+    nn.Linear, fp32 accumulation), then the route_topk routing of those logits
+    (trajectory/llada.py:228-234).  ``gate_weight`` is ``[E, H]`` bf16, E <= 64.
+    """
+    H = hidden_states.shape[-1]
+    x = hidden_states.reshape(-1, H)
+    if x.dtype != torch.bfloat16:
+        x = x.to(torch.bfloat16)
+    x = x.contiguous()
+    wg = gate_weight.to(torch.bfloat16).contiguous()
+    if wg.dim() != 2 or wg.shape[1] != H:
+        raise ValueError(f"gate_weight must be [experts, {H}], got {tuple(gate_weight.shape)}")
+    E = wg.shape[0]
+    if not 1 <= top_k <= E:
+        raise ValueError(f"top_k must lie in [1, {E}], got {top_k}")
+    device = _lib.require_hip(x, wg)
+    T = x.shape[0]
+    ids = torch.empty(T, top_k, dtype=torch.int32, device=device)
+    weights = torch.empty(T, top_k, dtype=torch.float32, device=device)
+    logits = torch.empty(T, E, dtype=torch.bfloat16, device=device) if return_logits else None
+    if T:
+        lib = _lib.load()
+        with torch.cuda.device(device):
+            rc = lib.lq_route_gemm_topk(_lib.ptr(x), _lib.ptr(wg), T, H, E, top_k, int(renormalize), _lib.ptr(ids),
+                                        _lib.ptr(weights), _lib.ptr(logits), _lib.stream(device))
+        _lib.check(rc, "route_gemm_topk")
+    return (ids, weights, logits) if return_logits else (ids, weights)
+
+
 def gather_topk_weights(gating_output: torch.Tensor, topk_ids: torch.Tensor,
                         renormalize: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
     """``(ids int32, weights fp32)`` with ``weights[t, j] = gating_output[t, topk_ids[t, j]]``."""
