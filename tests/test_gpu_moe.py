@@ -335,18 +335,20 @@ def test_streaming_many_experts(dev, E, T, k):
     assert_close(a, oracle_out(x, q1, q2, ids, w))
 
 
-@pytest.mark.parametrize("T,k", [(64, 8), (600, 8)])
-def test_moe_layer_front_end_matches_router_then_forward(dev, T, k):
-    """moe_layer: at T*k <= 2048 (8 rows per expert) the streaming GEMMs plan their own
-    blocks; T=600 (150 rows per expert) runs the plan kernel and the wide GEMMs; both
-    equal route_topk + fused_moe_packed."""
-    E, H, I = 32, 1024, 512
-    q1, q2 = make_layer(dev, E, H, I, 4, seed=T)
+@pytest.mark.parametrize("T,k,E,renorm", [(64, 8, 32, False), (600, 8, 32, False), (64, 8, 64, True),
+                                          (256, 8, 64, False), (3, 2, 64, True)])
+def test_moe_layer_front_end_matches_router_then_forward(dev, T, k, E, renorm):
+    """moe_layer (router kernel + GEMMs in one call): at T*k <= 2048 the streaming GEMMs plan
+    their own blocks; T=600 (150 rows per expert) runs the plan kernel and the wide GEMMs.
+    Both give the ids and output of route_topk + fused_moe_packed bit for bit, with and
+    without renormalized weights."""
+    H, I = 1024, 512
+    q1, q2 = make_layer(dev, E, H, I, 4, seed=T + E)
     g = torch.Generator().manual_seed(T + 1)
     x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
     logits = zipf_logits(T, E, seed=T).to(dev)
-    out, ids = moe_layer(x, logits, q1, q2, top_k=k)
-    ids2, w2 = route_topk(logits, k)
+    out, ids = moe_layer(x, logits, q1, q2, top_k=k, renormalize=renorm)
+    ids2, w2 = route_topk(logits, k, renormalize=renorm)
     assert torch.equal(ids, ids2)
     ref = fused_moe_packed(x, q1, q2, ids2, w2)
     assert torch.equal(out, ref)
