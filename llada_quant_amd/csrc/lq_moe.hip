@@ -692,7 +692,7 @@ __device__ __forceinline__ void wide_chunk(const WChunk<BITS> (&w)[NT], const fl
 
 template <int BITS, int NRT, bool FIRST, bool G128>
 __device__ __forceinline__ void wide_item(const MoeArgs &a, int e, int slice, int row0, int rows,
-                                          unsigned char *lds) {
+                                          unsigned char *lds, int *r_asg, float *r_wt) {
   static_assert(NRT == 2 || NRT == 4 || NRT == 8, "row tiles per block");
   constexpr int NQ = NRT * 256 / kWThreads;  // staged pieces per thread and chunk: NRT * 16 rows x 16 pieces
   constexpr int NT = kWT;
@@ -794,6 +794,15 @@ __device__ __forceinline__ void wide_item(const MoeArgs &a, int e, int slice, in
   // lg checks groups lg, lg + 4, ... of its tiles' rows, up to 4 * kChk
   // groups; longer rows take the exact-slow form throughout.
   constexpr int kChk = G128 ? 4 : 8;
+  // G2: the assignment and routing weight of each row (thread r < rows),
+  // fetched before the K loop and kept in LDS for the epilogue: their two
+  // dependent loads overlap the item's first loads instead of following
+  // the last chunk
+  int asg_r = 0;
+  float wt_r = 0.0f;
+  if constexpr (!FIRST) {
+    if (tid < rows) asg_r = a.sorted[row0 + tid];
+  }
   bool ok = ng <= 4 * kChk;
   {
     const __amdgpu_buffer_rsrc_t rs = ok ? srsrc : empty;
@@ -815,10 +824,20 @@ __device__ __forceinline__ void wide_item(const MoeArgs &a, int e, int slice, in
     WChunk<BITS> wb[2][NT];
     float sb[2][NT];
     u32x4 av[NQ];
+    if constexpr (!FIRST) {
+      if (tid < rows) wt_r = a.topk_w[asg_r];
+    }
+    __builtin_amdgcn_sched_barrier(0);
     load_a(0, av);
     __builtin_amdgcn_sched_barrier(0);
     load_w(0, wb[0], sb[0]);
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (!FIRST) {
+      if (tid < rows) {
+        r_asg[tid] = asg_r;
+        r_wt[tid] = wt_r;
+      }
+    }
     store_a(0, av);
     load_a(1, av);
     __builtin_amdgcn_sched_barrier(0);
@@ -868,8 +887,8 @@ __device__ __forceinline__ void wide_item(const MoeArgs &a, int e, int slice, in
       for (int j = 0; j < 4; ++j) {
         const int m = rt * 16 + 4 * lg + j;
         if (m < rows) {
-          const int asg = a.sorted[row0 + m];
-          const float wt = a.topk_w[asg];
+          const int asg = r_asg[m];
+          const float wt = r_wt[m];
           float *yrow = a.ybuf + static_cast<int64_t>(asg) * a.H + obase + lc;
 #pragma unroll
           for (int c = 0; c < NT; ++c) yrow[16 * c] = tot[rt][c][j] * wt;
@@ -886,6 +905,8 @@ template <int BITS, bool FIRST, bool G128>
 __global__ __launch_bounds__(kWThreads, 1) void moe_wide_kernel(MoeArgs a) {
   static_assert(kWT == 2, "G1 pairs the gate and up tile of each wave");
   __shared__ __align__(16) unsigned char lds[2 * kWStage];
+  __shared__ int r_asg[kWRows];    // G2: assignment and routing weight of each row of the item
+  __shared__ float r_wt[kWRows];
   const int nb = __builtin_amdgcn_readfirstlane(a.hdr->n_blk);
   const int per = FIRST ? a.I / kWF1 : a.H / kWR2;
   const int n = nb * per;
@@ -901,11 +922,11 @@ __global__ __launch_bounds__(kWThreads, 1) void moe_wide_kernel(MoeArgs a) {
     const int row0 = __builtin_amdgcn_readfirstlane(bi.y);
     const int rows = __builtin_amdgcn_readfirstlane(bi.z);
     if (rows <= 32)
-      wide_item<BITS, 2, FIRST, G128>(a, e, slice, row0, rows, lds);
+      wide_item<BITS, 2, FIRST, G128>(a, e, slice, row0, rows, lds, r_asg, r_wt);
     else if (rows <= 64)
-      wide_item<BITS, 4, FIRST, G128>(a, e, slice, row0, rows, lds);
+      wide_item<BITS, 4, FIRST, G128>(a, e, slice, row0, rows, lds, r_asg, r_wt);
     else
-      wide_item<BITS, 8, FIRST, G128>(a, e, slice, row0, rows, lds);
+      wide_item<BITS, 8, FIRST, G128>(a, e, slice, row0, rows, lds, r_asg, r_wt);
   }
 }
 
