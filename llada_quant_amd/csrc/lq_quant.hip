@@ -155,8 +155,38 @@ __device__ __forceinline__ float candidate_ratio(double max_shrink, int step, in
   return static_cast<float>(1.0 - max_shrink * static_cast<double>(step) / static_cast<double>(grid));
 }
 
-__device__ __forceinline__ float sq_err(float x, float safe, float qmin, float qmax) {
-  float v = x / safe;                    // work = wf / safe
+// The IEEE quotient RN(x / s) from y = RN(1 / s), computed once per candidate
+// scale (Markstein's division): q0 = RN(x y); r = x - s q is exact with an
+// FMA; after one correction q1 = RN(q0 + r0 y) lies within one ulp of x / s,
+// and then RN(q1 + r1 y) is the correctly rounded quotient.  That holds
+// without underflow or overflow, so the caller takes it only for a normal,
+// finite s with a normal reciprocal and |x| >= 2^-100 or x = 0 (the
+// quotients of a group are bounded by 2 Qmax, the residuals then stay
+// normal); other lanes divide.
+struct RecipScale {
+  float s, y;
+  bool ok;  // the Markstein quotient applies for this scale
+};
+__device__ __forceinline__ RecipScale recip_scale(float s) {
+  const float y = 1.0f / s;
+  const bool ok = s >= 0x1p-126f && s <= 0x1p125f && y >= 0x1p-126f;
+  return {s, y, ok};
+}
+__device__ __forceinline__ float div_rs(float x, const RecipScale &d) {
+  float q;
+  if (d.ok && (x == 0.0f || fabsf(x) >= 0x1p-100f)) {
+    const float q0 = x * d.y;
+    const float q1 = fmaf(fmaf(-q0, d.s, x), d.y, q0);
+    q = fmaf(fmaf(-q1, d.s, x), d.y, q1);
+  } else {
+    q = x / d.s;
+  }
+  return q;
+}
+
+__device__ __forceinline__ float sq_err(float x, const RecipScale &d, float qmin, float qmax) {
+  const float safe = d.s;
+  float v = div_rs(x, d);                // work = wf / safe
   v = rintf(v);                          // round_ (half to even)
   v = fminf(fmaxf(v, qmin), qmax);       // clamp_
   v = v * safe;                          // mul_(safe)
@@ -236,11 +266,12 @@ __global__ __launch_bounds__(kBlock) void quant_group8_kernel(QuantArgs a) {
     for (int step = 0; step < a.grid; ++step) {
       const float cand = amax_s * candidate_ratio(a.max_shrink, step, a.grid);
       const float safe = cand > 0.0f ? cand : 1.0f;
+      const RecipScale rs = recip_scale(safe);
       float acc0 = 0.0f, acc1 = 0.0f, acc2 = 0.0f, acc3 = 0.0f;
 #pragma unroll
       for (int i = 0; i < MAXV; ++i) {
         if (i < vs) {
-          const float e = sq_err(x[i], safe, qmin, qmax);
+          const float e = sq_err(x[i], rs, qmin, qmax);
           if (i < rows4) {
             if ((i & 3) == 0) acc0 += e;
             else if ((i & 3) == 1) acc1 += e;
@@ -382,7 +413,8 @@ __global__ __launch_bounds__(kBlock) void quant_generic_kernel(QuantArgs a) {
     for (int step = 0; step < a.grid; ++step) {
       const float cand = amax_s * candidate_ratio(a.max_shrink, step, a.grid);
       const float safe = cand > 0.0f ? cand : 1.0f;
-      auto err = [&](int64_t i) { return sq_err(load_f32<WDT>(a.w, base + i), safe, qmin, qmax); };
+      const RecipScale rs = recip_scale(safe);
+      auto err = [&](int64_t i) { return sq_err(load_f32<WDT>(a.w, base + i), rs, qmin, qmax); };
       const float e = torch_cpu_sum(err, a.n);
       if (e < best_err) {
         best_err = e;

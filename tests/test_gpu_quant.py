@@ -203,3 +203,24 @@ def test_zero_tensor_quantizes_to_zero(dev):
     for search in ("amax", "mse"):
         q = quantize_tensor(torch.zeros(4, 8, 16, device=dev), bits=8, group_size=8, scale_search=search)
         assert torch.all(q.q == 0) and torch.all(q.scale == 0)
+
+
+@pytest.mark.parametrize("bits,group", [(4, 128), (8, 128), (4, 32)])
+def test_mse_search_extreme_magnitudes_match_the_oracle(dev, bits, group):
+    """The MSE search divides by each candidate scale through its reciprocal (Markstein's
+    correctly rounded quotient), falling back to the IEEE division where that does not
+    apply.  Groups here span 2^-149 .. 2^120 in magnitude, with subnormal weights, zeros
+    and subnormal scales: codes and scales must equal the oracle's (IEEE division) bit
+    for bit."""
+    rng = np.random.default_rng(bits + group)
+    rows, K = 96, 256
+    mag = np.exp2(rng.integers(-149, 121, size=(rows * K // group, 1))).astype(np.float64)
+    w = (rng.standard_normal((rows * K // group, group)) * mag).reshape(rows, K)
+    w[rng.random(w.shape) < 0.05] = 0.0
+    w[::7, :group] = 0.0  # whole zero groups
+    w = np.clip(w, -3e38, 3e38).astype(np.float32)
+    wt = torch.from_numpy(w).to(dev)
+    res = quantize_tensor(wt, bits=bits, group_size=group, scale_search="mse", search_grid=16)
+    oq, os_, _ = O.quantize(w, bits, group, "mse", grid=16, w_dtype=O.F32)
+    assert np.array_equal(res.scale.cpu().numpy(), os_)
+    assert np.array_equal(res.q.cpu().numpy(), oq)
