@@ -1767,7 +1767,7 @@ __device__ __forceinline__ void plan_body(const PlanArgs &p, IdAt id_at) {
 // scans the totals into offsets, and scatters its own segment stably from
 // offsets + prefix; workgroup 0 also writes counts, offsets and the block
 // table.
-constexpr int kPlanSeg = 4 * kPlanBlock;
+constexpr int kPlanSeg = kPlanBlock;  // one chunk per segment: no chunk loop in the scatter
 
 __global__ __launch_bounds__(kPlanBlock) void plan_count_kernel(PlanArgs p, int32_t *seg_cnt) {
   __shared__ int hist[kMaxExperts];
@@ -1776,14 +1776,15 @@ __global__ __launch_bounds__(kPlanBlock) void plan_count_kernel(PlanArgs p, int3
   for (int e = tid; e < E; e += kPlanBlock) hist[e] = 0;
   __syncthreads();
   const int64_t a0 = static_cast<int64_t>(blockIdx.x) * kPlanSeg;
-  int idv[4];
+  constexpr int kPer = kPlanSeg / kPlanBlock;
+  int idv[kPer];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < kPer; ++j) {
     const int64_t a = a0 + j * kPlanBlock + tid;
     idv[j] = a < p.N ? p.ids[a] : -1;
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+  for (int j = 0; j < kPer; ++j)
     if (idv[j] >= 0 && idv[j] < E) atomicAdd(&hist[idv[j]], 1);
   __syncthreads();
   for (int e = tid; e < E; e += kPlanBlock) seg_cnt[static_cast<int64_t>(blockIdx.x) * E + e] = hist[e];

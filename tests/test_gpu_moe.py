@@ -251,8 +251,8 @@ def test_gemm_family_threshold(dev, T):
 
 @pytest.mark.parametrize("T,k,E", [(2600, 4, 8), (1100, 8, 16)])
 def test_multi_workgroup_plan(dev, T, k, E):
-    """More than 4096 routed rows: the expert plan runs as one workgroup per segment
-    of 4096 assignments (count, then scatter); the whole output is checked against
+    """More than 1024 routed rows: the expert plan runs as one workgroup per segment
+    of 1024 assignments (count, then scatter); the whole output is checked against
     the oracle, and the wide, general and streaming GEMMs (all fed by that plan) agree."""
     H, I = 512, 512
     q1, q2 = make_layer(dev, E, H, I, 4, seed=T + E)
