@@ -691,7 +691,7 @@ __device__ __forceinline__ void wide_chunk(const WChunk<BITS> (&w)[NT], const fl
 }
 
 template <int BITS, int NRT, bool FIRST, bool G128>
-__device__ __forceinline__ void wide_item(const MoeArgs &a, int e, int slice, int row0, int rows,
+__device__ __forceinline__ void wide_item(const MoeArgs &a, int e, int slice, int row0, int rows, int ks,
                                           unsigned char *lds, int *r_asg, float *r_wt) {
   static_assert(NRT == 2 || NRT == 4 || NRT == 8, "row tiles per block");
   constexpr int NQ = NRT * 256 / kWThreads;  // staged pieces per thread and chunk: NRT * 16 rows x 16 pieces
@@ -702,7 +702,12 @@ __device__ __forceinline__ void wide_item(const MoeArgs &a, int e, int slice, in
   const int lc = lane & 15;
   const int lg = lane >> 4;
   const int K = FIRST ? a.H : a.I;
-  const int nk = K / kKC;  // K is a multiple of 256 on this path (host-checked): nk is even
+  // G2 may split K (ksplit > 1): this item sums chunks [c0, c0 + nk) of the
+  // full K, nk even (host-checked), and writes its partial sums to slot
+  // asg * ksplit + ks; chunk i below is chunk c0 + i
+  const int ksplit = FIRST ? 1 : a.ksplit;
+  const int nk = K / kKC / ksplit;  // K / ksplit is a multiple of 256 on this path (host-checked): nk is even
+  const int c0 = ks * nk;
 
   // ---- token rows: piece tid + 512 q of a chunk is row r = piece >> 4,
   // 16-byte piece lc of the row's 128 K values, stored at slot lc ^ (r & 15)
@@ -723,7 +728,7 @@ __device__ __forceinline__ void wide_item(const MoeArgs &a, int e, int slice, in
   auto load_a = [&](int i, u32x4(&v)[NQ]) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t r = i < nk ? arsrc : empty;
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) v[q] = __builtin_amdgcn_raw_buffer_load_b128(r, avoff[q], i * kKC * 2, 0);
+    for (int q = 0; q < NQ; ++q) v[q] = __builtin_amdgcn_raw_buffer_load_b128(r, avoff[q], (c0 + i) * kKC * 2, 0);
   };
   auto store_a = [&](int i, const u32x4(&v)[NQ]) __attribute__((always_inline)) {
     unsigned char *buf = lds + (i & 1) * kWStage;
@@ -760,16 +765,18 @@ __device__ __forceinline__ void wide_item(const MoeArgs &a, int e, int slice, in
 #pragma unroll
     for (int c = 0; c < NT; ++c) {
       if constexpr (BITS == 4) {
-        w[c].v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, wvoff[c], i * kChunkBytes, 0));
+        w[c].v = __builtin_bit_cast(uint4,
+                                    __builtin_amdgcn_raw_buffer_load_b128(rw, wvoff[c], (c0 + i) * kChunkBytes, 0));
       } else {
-        w[c].v0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, wvoff[c], i * kChunkBytes, 0));
-        w[c].v1 =
-            __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, wvoff[c] + 16, i * kChunkBytes, 0));
+        w[c].v0 = __builtin_bit_cast(uint4,
+                                     __builtin_amdgcn_raw_buffer_load_b128(rw, wvoff[c], (c0 + i) * kChunkBytes, 0));
+        w[c].v1 = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, wvoff[c] + 16, (c0 + i) * kChunkBytes, 0));
       }
       if constexpr (G128) {
-        sc[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, svoff[c], i * 4, 0));
+        sc[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, svoff[c], (c0 + i) * 4, 0));
       } else {
-        const int sidx = (i * kKC + 32 * lg) / G;  // group of this lane's 32 K values
+        const int sidx = ((c0 + i) * kKC + 32 * lg) / G;  // group of this lane's 32 K values
         sc[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, svoff[c] + 4 * sidx, 0, 0));
       }
     }
@@ -791,8 +798,9 @@ __device__ __forceinline__ void wide_item(const MoeArgs &a, int e, int slice, in
   // the two steps past the last chunk load out of range.
   // Dequant choice: one per item and wave (FAST needs dq_fast_ok for every
   // scale the wave meets), so each K loop holds one form only.  Lane group
-  // lg checks groups lg, lg + 4, ... of its tiles' rows, up to 4 * kChk
-  // groups; longer rows take the exact-slow form throughout.
+  // lg checks groups g0 + lg, g0 + lg + 4, ... of the item's K range in its
+  // tiles' rows, up to 4 * kChk groups; longer ranges take the exact-slow
+  // form throughout.
   constexpr int kChk = G128 ? 4 : 8;
   // G2: the assignment and routing weight of each row (thread r < rows),
   // fetched before the K loop and kept in LDS for the epilogue: their two
@@ -803,16 +811,18 @@ __device__ __forceinline__ void wide_item(const MoeArgs &a, int e, int slice, in
   if constexpr (!FIRST) {
     if (tid < rows) asg_r = a.sorted[row0 + tid];
   }
-  bool ok = ng <= 4 * kChk;
+  // (the groups of this item's K range [c0, c0 + nk) chunks: [g0, g1))
+  const int g0 = c0 * kKC / G, g1 = min(ng, ((c0 + nk) * kKC + G - 1) / G);
+  bool ok = g1 - g0 <= 4 * kChk;
   {
     const __amdgpu_buffer_rsrc_t rs = ok ? srsrc : empty;
     float chk[NT][kChk];
 #pragma unroll
     for (int c = 0; c < NT; ++c)
 #pragma unroll
-      for (int j = 0; j < kChk; ++j)  // groups past the row read as 0 (fast)
-        chk[c][j] = __builtin_bit_cast(
-            float, __builtin_amdgcn_raw_buffer_load_b32(lg + 4 * j < ng ? rs : empty, svoff[c], 4 * (lg + 4 * j), 0));
+      for (int j = 0; j < kChk; ++j)  // groups past the range read as 0 (fast)
+        chk[c][j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                  g0 + lg + 4 * j < g1 ? rs : empty, svoff[c], 4 * (g0 + lg + 4 * j), 0));
 #pragma unroll
     for (int c = 0; c < NT; ++c)
 #pragma unroll
@@ -889,7 +899,7 @@ __device__ __forceinline__ void wide_item(const MoeArgs &a, int e, int slice, in
         if (m < rows) {
           const int asg = r_asg[m];
           const float wt = r_wt[m];
-          float *yrow = a.ybuf + static_cast<int64_t>(asg) * a.H + obase + lc;
+          float *yrow = a.ybuf + (static_cast<int64_t>(asg) * ksplit + ks) * a.H + obase + lc;
 #pragma unroll
           for (int c = 0; c < NT; ++c) yrow[16 * c] = tot[rt][c][j] * wt;
         }
@@ -908,7 +918,8 @@ __global__ __launch_bounds__(kWThreads, 1) void moe_wide_kernel(MoeArgs a) {
   __shared__ int r_asg[kWRows];    // G2: assignment and routing weight of each row of the item
   __shared__ float r_wt[kWRows];
   const int nb = __builtin_amdgcn_readfirstlane(a.hdr->n_blk);
-  const int per = FIRST ? a.I / kWF1 : a.H / kWR2;
+  const int ksplit = FIRST ? 1 : a.ksplit;
+  const int per = (FIRST ? a.I / kWF1 : a.H / kWR2) * ksplit;  // items per block: slices x K slices
   const int n = nb * per;
   const int xcd = blockIdx.x & 7;
   const int gx = gridDim.x >> 3;
@@ -916,17 +927,19 @@ __global__ __launch_bounds__(kWThreads, 1) void moe_wide_kernel(MoeArgs a) {
   const int end = min(n, (xcd + 1) * n8);
   for (int t = xcd * n8 + static_cast<int>(blockIdx.x >> 3); t < end; t += gx) {
     const int blk = t / per;
-    const int slice = t - blk * per;
+    const int rem = t - blk * per;
+    const int slice = rem / ksplit;
+    const int ks = rem - slice * ksplit;
     const int4 bi = a.blocks[blk];
     const int e = __builtin_amdgcn_readfirstlane(bi.x);
     const int row0 = __builtin_amdgcn_readfirstlane(bi.y);
     const int rows = __builtin_amdgcn_readfirstlane(bi.z);
     if (rows <= 32)
-      wide_item<BITS, 2, FIRST, G128>(a, e, slice, row0, rows, lds, r_asg, r_wt);
+      wide_item<BITS, 2, FIRST, G128>(a, e, slice, row0, rows, ks, lds, r_asg, r_wt);
     else if (rows <= 64)
-      wide_item<BITS, 4, FIRST, G128>(a, e, slice, row0, rows, lds, r_asg, r_wt);
+      wide_item<BITS, 4, FIRST, G128>(a, e, slice, row0, rows, ks, lds, r_asg, r_wt);
     else
-      wide_item<BITS, 8, FIRST, G128>(a, e, slice, row0, rows, lds, r_asg, r_wt);
+      wide_item<BITS, 8, FIRST, G128>(a, e, slice, row0, rows, ks, lds, r_asg, r_wt);
   }
 }
 
@@ -2410,11 +2423,22 @@ int linear_ksplit(int64_t M, int K, int N) {
   return S;
 }
 
-// the wide kernels take a QuantLinear when their items alone fill the GPU
+// the wide kernels take a QuantLinear from 128 rows on (their 128-row
+// dequant amortisation; measured on MI355X, 8192 x 8192 INT8: the general
+// kernel is ahead at 64 rows), with K slices of whole 256-wide pairs of
+// chunks until about 512 items exist (at most 16)
 bool linear_wide(int64_t M, int K, int N, int flags) {
   if (flags & LQ_MOE_WIDE_KERNEL) return true;
   if (flags & LQ_MOE_GENERAL_KERNEL) return false;
-  return wide_eligible(N, K, 0) && M >= kWideMinRows && ceil_div(M, kWRows) * (N / kWR2) >= 256;
+  return wide_eligible(N, K, 0) && M >= kWRows;
+}
+
+int linear_wide_ksplit(int64_t M, int K, int N) {
+  const int64_t items = ceil_div(M, kWRows) * (N / kWR2);
+  const int npair = K / (2 * kKC);
+  int S = 1;
+  while (items * S < 512 && S < 16 && npair % (2 * S) == 0) S *= 2;
+  return S;
 }
 
 // QuantLinear (runtime/linear.py:127-131): out = bf16(x . dequant(W)^T) with
@@ -2424,7 +2448,8 @@ bool linear_wide(int64_t M, int K, int N, int flags) {
 // items fill the GPU, else general with K slices), combine.
 extern "C" size_t lq_linear_workspace_bytes(int64_t M, int K, int N) {
   if (M < 0 || K <= 0 || N <= 0) return 0;
-  return ws_layout(M, N, K, 1, linear_ksplit(M, K, N)).total;
+  return ws_layout(M, N, K, 1, std::max(linear_ksplit(M, K, N), K % (2 * kKC) == 0 ? linear_wide_ksplit(M, K, N) : 1))
+      .total;
 }
 
 extern "C" int lq_quant_linear(const void *x, int64_t M, int K, int N, const int8_t *q, const float *s, int bits,
@@ -2455,8 +2480,9 @@ extern "C" int lq_quant_linear(const void *x, int64_t M, int K, int N, const int
   if (!aligned16(x) || !aligned16(q) || !aligned16(workspace) || !aligned16(out))
     return fail(LQ_ERR_VALUE, "quant_linear: x, qweight, workspace and out must be 16-byte aligned");
   const bool wide = linear_wide(M, K, N, flags);
-  const int S = wide ? 1 : linear_ksplit(M, K, N);
-  const WsLayout w = ws_layout(M, N, K, 1, linear_ksplit(M, K, N));
+  const int S = wide ? linear_wide_ksplit(M, K, N) : linear_ksplit(M, K, N);
+  const WsLayout w = ws_layout(
+      M, N, K, 1, std::max(linear_ksplit(M, K, N), K % (2 * kKC) == 0 ? linear_wide_ksplit(M, K, N) : 1));
   if (ws_bytes < w.total)
     return fail(LQ_ERR_VALUE, "quant_linear: workspace too small (" + std::to_string(ws_bytes) + " < " +
                                   std::to_string(w.total) + ")");
@@ -2506,7 +2532,7 @@ extern "C" int lq_quant_linear(const void *x, int64_t M, int K, int N, const int
   a.ksplit = S;
   const int64_t blocks = max_blocks_for(M, 1, 1);
   if (wide) {
-    const int64_t items = (1 + M / kWRows) * (N / kWR2);
+    const int64_t items = (1 + M / kWRows) * (N / kWR2) * S;
     const bool g128 = a.g2 == kKC;
     if (bits == 4 && g128)
       moe_wide_kernel<4, false, true><<<wide_grid<4, false, true>(items), kWThreads, 0, st>>>(a);
