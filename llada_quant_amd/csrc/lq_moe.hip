@@ -1859,16 +1859,28 @@ __global__ __launch_bounds__(256) void permute_rows_kernel(const uint16_t *__res
 }
 
 // QuantLinear set-up: x [M, K] -> act [M, K] in the GEMMs' K-slot order
-// (8 values per thread), every row routed to expert 0 with weight 1.0
+// (8 values per thread), the nslot routing slots all expert 0 with weight
+// 1.0, and the plan of one expert, which is the identity: sorted / srow
+// [i] = i, blocks of br rows [b br, b br + br) (the plan kernel's output
+// for these ids, without its launch)
 __global__ __launch_bounds__(256) void linear_setup_kernel(const uint16_t *__restrict__ x, int64_t n8, int64_t M,
-                                                           uint16_t *__restrict__ act, int32_t *__restrict__ ids,
-                                                           float *__restrict__ weights) {
+                                                           int64_t nslot, uint16_t *__restrict__ act,
+                                                           int32_t *__restrict__ ids, float *__restrict__ weights,
+                                                           int32_t *__restrict__ sorted, int32_t *__restrict__ srow,
+                                                           int4 *__restrict__ blocks, PlanHeader *hdr, int br) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n8) reinterpret_cast<uint4 *>(act)[i] = permute_kslots(reinterpret_cast<const uint4 *>(x)[i]);
-  if (i < M) {
+  if (i < nslot) {
     ids[i] = 0;
     weights[i] = 1.0f;
   }
+  if (i < M) {
+    sorted[i] = static_cast<int32_t>(i);
+    srow[i] = static_cast<int32_t>(i);
+  }
+  const int64_t nb = (M + br - 1) / br;
+  if (i < nb) blocks[i] = make_int4(0, static_cast<int>(i * br), static_cast<int>(min<int64_t>(br, M - i * br)), 0);
+  if (i == 0) hdr->n_blk = static_cast<int32_t>(nb);
 }
 
 // ---------------------------------------------------------------------------
@@ -2491,23 +2503,12 @@ extern "C" int lq_quant_linear(const void *x, int64_t M, int K, int N, const int
   float *weights = reinterpret_cast<float *>(ws + w.weights);
   uint16_t *act = reinterpret_cast<uint16_t *>(ws + w.act);
   const int64_t n8 = M * K / 8;
-  linear_setup_kernel<<<static_cast<int>(ceil_div(std::max(n8, M * S), 256)), 256, 0, st>>>(
-      static_cast<const uint16_t *>(x), n8, M * S, act, ids, weights);
-  int rc = check_launch("quant_linear_setup");
-  if (rc) return rc;
   PlanArgs p = plan_args(ids, M, 1, 1, ws, w);
   p.block_rows = wide ? kWRows : kRowsMax;
-  const int64_t nseg = ceil_div(M, kPlanSeg);
-  if (nseg > 1) {
-    int32_t *segcnt = reinterpret_cast<int32_t *>(ws + w.segcnt);
-    plan_count_kernel<<<static_cast<int>(nseg), kPlanBlock, 0, st>>>(p, segcnt);
-    rc = check_launch("quant_linear_plan_count");
-    if (rc) return rc;
-    plan_scatter_kernel<<<static_cast<int>(nseg), kPlanBlock, 0, st>>>(p, segcnt, static_cast<int>(nseg));
-  } else {
-    plan_kernel<<<1, kPlanBlock, 0, st>>>(p);
-  }
-  rc = check_launch("quant_linear_plan");
+  linear_setup_kernel<<<static_cast<int>(ceil_div(std::max(n8, M * S), 256)), 256, 0, st>>>(
+      static_cast<const uint16_t *>(x), n8, M, M * S, act, ids, weights, p.sorted, p.srow, p.blocks, p.hdr,
+      p.block_rows);
+  int rc = check_launch("quant_linear_setup");
   if (rc) return rc;
   MoeArgs a{};
   a.q2 = q;
