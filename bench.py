@@ -65,8 +65,9 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-gpu-baseline", action="store_true", help="skip the dequantize-then-GEMM leg")
     p.add_argument("--seed", type=int, default=0)
-    p.add_argument("--kernel", choices=("auto", "stream", "general", "wide"), default="auto",
-                   help="GEMM family (auto: the library's own choice for the shape)")
+    p.add_argument("--kernel", choices=("auto", "stream", "fused", "general", "wide"), default="auto",
+                   help="GEMM family (auto: the library's own choice for the shape; fused: the streaming family "
+                        "as one launch, the fused layer kernel)")
     p.add_argument("--tokens", type=int, default=0, help="override the configuration's token count")
     p.add_argument("--folded", action="store_true",
                    help="time the LQ_MOE_FOLDED_SCALES form (integer codes, fp32 group scale) as the headline")
@@ -111,6 +112,7 @@ def pmc_traffic(config, form, kernel="gemm1"):
 
 
 KERNEL_NAMES = {
+    "fused": "moe_fused_kernel (route + plan + GEMM1 + GEMM2 + combine in one launch, W1/W2 streamed per CU)",
     "wide": "moe_wide_kernel<G1> (blocks of <= 128 rows, 4 weight tiles x 8 row tiles per wave, SwiGLU epilogue)",
     "stream": "moe_stream_kernel<G1> (W1 gate and up tiles streamed per CU)",
     "general": "moe_gemm_kernel<G1> (W1 gate+up, SwiGLU epilogue; persistent)",
@@ -487,7 +489,7 @@ def main():
     lib = _lib.load()
     stream = torch.cuda.current_stream(dev)
     ws_bytes = workspace_bytes(T, H, I, E, k)
-    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    workspace = _lib.moe_workspace(ws_bytes, dev)
     out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
     ids = torch.empty(T, k, dtype=torch.int32, device=dev)
 
@@ -505,8 +507,9 @@ def main():
     hip = Hip()
     hip.lib.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
     hip_stream = ctypes.c_void_p(stream.cuda_stream)
-    # stage boundaries of one lq_moe_layer call: 0 start, 1 route, 2 plan (a marker only when
-    # the GEMMs plan their own blocks), 3 GEMM1, 4 GEMM2 (+SwiGLU, routed weight), 5 combine
+    # stage boundaries of one lq_moe_layer call: 0 start, 1 route, 2 plan, 3 GEMM1, 4 GEMM2
+    # (+SwiGLU, routed weight), 5 combine.  The fused layer kernel is one launch: its time is the
+    # GEMM1 stage, the others record no kernel (route and plan too when it routes in-kernel)
     n_marks = 6
 
     def timed(calls, steps, warmup):
@@ -549,7 +552,8 @@ def main():
 
     family = kernel_family(cfg, args.folded, args.kernel)
     kflag = {"wide": _lib.LQ_MOE_WIDE_KERNEL, "general": _lib.LQ_MOE_GENERAL_KERNEL,
-             "stream": _lib.LQ_MOE_STREAM_KERNEL}.get(args.kernel, 0)
+             "stream": _lib.LQ_MOE_STREAM_KERNEL,
+             "fused": _lib.LQ_MOE_STREAM_KERNEL | _lib.LQ_MOE_FUSED_LAYER}.get(args.kernel, 0)
     calls = make_calls((_lib.LQ_MOE_FOLDED_SCALES if args.folded else 0) | kflag)
     wall0 = time.perf_counter()
     ms_per_step = timed(calls, args.steps, args.warmup)
@@ -560,12 +564,15 @@ def main():
     layer_b, g1_b, g2_b = layer_bytes(cfg, n_active)
     gemm1_ms = stage_ms[2]
     kname = KERNEL_NAMES[family]
-    traffic = pmc_traffic(args.config, "folded" if args.folded else "exact")
+    traffic = pmc_traffic(args.config, "folded" if args.folded else "exact",
+                          "fused" if family == "fused" else "gemm1")
     if cfg["bound"] == "hbm":
-        achieved = g1_b / (gemm1_ms / 1e3) / 1e9
+        # the dominant kernel: GEMM1, or the fused kernel, which is the whole layer
+        kb = layer_b if family == "fused" else g1_b
+        achieved = kb / (gemm1_ms / 1e3) / 1e9
         roofline = {"kernel": kname, "bound": "hbm", "achieved": round(achieved, 1), "peak": MI355X_HBM_GBPS,
                     "unit": "GB/s", "frac": round(achieved / MI355X_HBM_GBPS, 4), "traffic": traffic,
-                    "algorithmic_bytes": g1_b, "avg_ms": round(gemm1_ms, 5)}
+                    "algorithmic_bytes": kb, "avg_ms": round(gemm1_ms, 5)}
     else:
         flops = 2.0 * T * k * 2 * I * H
         achieved = flops / (gemm1_ms / 1e3) / 1e12
@@ -573,12 +580,21 @@ def main():
                     "unit": "TFLOP/s", "frac": round(achieved / MI355X_BF16_TFLOPS, 4), "traffic": traffic,
                     "algorithmic_flops": flops, "avg_ms": round(gemm1_ms, 5)}
     stages = {name: round(v, 5) for name, v in zip(("route", "plan", "gemm1", "gemm2", "combine"), stage_ms)}
-    stages["gemm2_gbps"] = round(g2_b / (stage_ms[3] / 1e3) / 1e9, 1)
+    if family != "fused":
+        stages["gemm2_gbps"] = round(g2_b / (stage_ms[3] / 1e3) / 1e9, 1)
     # the other weight form (the wide kernels take exact weights only)
     other_calls = make_calls(0 | kflag if args.folded else
                              _lib.LQ_MOE_FOLDED_SCALES | (kflag if args.kernel in ("general", "stream") else 0))
     other_ms = timed(other_calls, max(10, args.steps // 4), 3)
     other_stage = staged(other_calls, max(10, args.steps // 4))
+    # the whole layer as one launch (the fused layer kernel), where it applies
+    fused_extra = None
+    if family == "stream" and not args.folded and E <= 64 and T * k <= 2048:
+        fcalls = make_calls(_lib.LQ_MOE_FUSED_LAYER | kflag)
+        f_ms = timed(fcalls, max(10, args.steps // 2), 5)
+        fused_extra = {"ms_per_step": round(f_ms, 5), "value": round(T / (f_ms / 1e3), 1), "unit": "tokens/s",
+                       "kernel": "moe_fused_kernel (route + plan + GEMM1 + GEMM2 + combine, one launch)",
+                       "layer_gbps": round(layer_b / (f_ms / 1e3) / 1e9, 1)}
 
     result = {
         "metric": "MoE-layer tokens/s W4A16 64E top-8 H2048; % HBM/MFMA roofline",
@@ -611,6 +627,8 @@ def main():
             "ms_per_step": round(other_ms, 5), "gemm1_ms": round(other_stage[2], 5),
             "gemm2_ms": round(other_stage[3], 5), "value": round(T / (other_ms / 1e3), 1), "unit": "tokens/s"},
     }
+    if fused_extra is not None:
+        result["fused_layer"] = fused_extra
     if not args.no_gpu_baseline:
         result["gpu_dequant_then_gemm"] = gpu_dequant_then_gemm(torch, cfg, layers, x, logits,
                                                                 max(5, args.steps // 10), 3)

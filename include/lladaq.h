@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define LQ_ABI_VERSION 2
+#define LQ_ABI_VERSION 3
 
 /* status codes */
 #define LQ_OK 0
@@ -47,6 +47,8 @@ extern "C" {
 #define LQ_MOE_GENERAL_KERNEL 2 /* use the general GEMM kernels for every shape (same results) */
 #define LQ_MOE_WIDE_KERNEL 4    /* use the wide (matrix-core) GEMM kernels (same results; H % 256, I % 256) */
 #define LQ_MOE_STREAM_KERNEL 8  /* use the streaming (bandwidth) GEMM kernels (same results; see lq_moe_forward) */
+#define LQ_MOE_FUSED_LAYER 16 /* streaming family, E <= 64, T*k <= 2048: the whole layer as one launch
+                                 (moe_fused_kernel; same results) instead of GEMM1, GEMM2, combine */
 
 /* scale search codes (QuantConfig.scale_search) */
 #define LQ_SCALE_AMAX 0
@@ -159,8 +161,39 @@ int lq_moe_permute(const int32_t *topk_ids, int64_t T, int k, int E,
                    int32_t *counts, int32_t *offsets, int32_t *sorted,
                    lq_stream_t stream);
 
-/* Bytes of workspace lq_moe_forward needs for this shape. */
+/*
+ * Bytes of workspace lq_moe_forward / lq_moe_layer need for this shape.
+ * A workspace starts with a sync region of lq_moe_sync_bytes() bytes (the
+ * same size and place for every shape): a status word at offset 0 and the
+ * counters through which the workgroups of the fused layer kernel hand data
+ * to each other.  It must be zero before the first call on a workspace
+ * (lq_moe_workspace_init, or allocate it zeroed), and every call leaves it
+ * zero; the rest of the workspace is scratch.  One workspace serves one
+ * stream at a time.  (No counterpart in the reference: its dequantize-then-
+ * fused_moe path allocates through torch.)
+ */
 size_t lq_moe_workspace_bytes(int64_t T, int H, int I, int E, int k);
+
+/* Size of the sync region at the start of every MoE workspace. */
+size_t lq_moe_sync_bytes(void);
+
+/* Zero the sync region of a workspace (hipMemsetAsync on `stream`).  Call once
+ * after allocating it; not under graph capture. */
+int lq_moe_workspace_init(void *workspace, lq_stream_t stream);
+
+/*
+ * Read the status word of a workspace after the calls on `stream` (this call
+ * synchronises the stream).  Bit 1: a wave of a streaming GEMM gave up
+ * waiting for another wave's partial sums; bit 2: the fused layer kernel
+ * gave up waiting for its row block's GEMM1 tiles; bit 4: ... for the other
+ * workgroups before its combine; bit 8: ... for the routing of every token
+ * (its workgroups were not all resident at once, e.g. the GPU was shared).
+ * Any of them means the output of some call since the last clear is wrong.
+ * clear != 0 zeroes the whole sync region when the word is not zero.
+ * Debugging aid; no counterpart in the reference.
+ */
+int lq_moe_status(const void *workspace, uint32_t *status, int clear,
+                  lq_stream_t stream);
 
 /*
  * The quantized expert layer (fused_moe with packed weights):
@@ -188,9 +221,12 @@ size_t lq_moe_workspace_bytes(int64_t T, int H, int I, int E, int k);
  *   workspace of ws_bytes >= lq_moe_workspace_bytes(T, H, I, E, k)
  * Requires H % 128 == 0, I % 64 == 0, group lengths (after the per-row
  * fallback) that are multiples of 32, and T <= 262144.  Kernels on `stream`:
- * the expert plan (skipped when T*k <= 2048 and the streaming GEMMs derive it
- * themselves), GEMM1, GEMM2, combine; the general GEMMs add an x permute in
- * front.  No host synchronisation.
+ * small layers of the streaming family (T*k <= 2048, exact weights) run as
+ * ONE launch, the fused layer kernel (plan, GEMM1, GEMM2 and combine, the
+ * workgroups handing data to each other through the workspace's sync
+ * region); otherwise the expert plan, GEMM1, GEMM2, combine, with an x
+ * permute in front for the general and wide GEMMs.  No host
+ * synchronisation.
  */
 int lq_moe_forward(const void *x, int64_t T, int H, int I, int E, int k,
                    const int8_t *q1, const float *s1, const int8_t *q2,
@@ -203,7 +239,10 @@ int lq_moe_forward(const void *x, int64_t T, int H, int I, int E, int k,
  * The whole MoE layer from router logits: lq_route_topk into the workspace,
  * then lq_moe_forward (the TritonFusedMoEBlock.forward sequence after the
  * gate: softmax -> topk -> fused_moe; trajectory/llada.py:228-234 and
- * INFERENCE_REPO_CHANGES.md:110-111).  One host call, one stream.
+ * INFERENCE_REPO_CHANGES.md:110-111).  One host call, one stream.  When the
+ * fused layer kernel takes the layer and T <= 64, E <= 64, that one launch
+ * also routes (every workgroup routes all tokens with lq_route_topk's
+ * arithmetic), so the layer is a single kernel.
  *   logits [T, E] in logits_dtype; topk_ids_out (optional, [T, k] int32)
  *   receives the routing; all other arguments as lq_moe_forward.
  */
@@ -240,8 +279,10 @@ int lq_moe_profile_events(void *const *events, int n_events);
  * Requires N % 128 == 0, K % 64 == 0, group length % 32 == 0, M <= 262144.
  * flags: 0, LQ_MOE_WIDE_KERNEL or LQ_MOE_GENERAL_KERNEL (same results).  The
  * bias of the reference module is added by the caller (a bf16 add after the
- * bf16 product, as the reference does).  Kernels on `stream`: set-up, plan,
- * GEMM, combine; no host synchronisation, no device allocation.
+ * bf16 product, as the reference does).  Kernels on `stream`: set-up (which
+ * also writes the one-expert plan), GEMM (the wide family from 128 rows on,
+ * else the general one; both may split K into slices), combine; no host
+ * synchronisation, no device allocation.
  */
 int lq_quant_linear(const void *x, int64_t M, int K, int N, const int8_t *q,
                     const float *s, int bits, int64_t group, int flags,

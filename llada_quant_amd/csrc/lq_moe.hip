@@ -105,7 +105,23 @@ struct MoeArgs {
   int H, I, E, k;
   int g1, ng1, g2, ng2;    // group length and groups per row of w1 / w2
   int ksplit;              // general G2 only: K slices per item (partial sums to ybuf slot asg * ksplit + ks)
+  // fused layer kernel only
+  const void *logits;      // [T, E] router logits (dtype ldt), or nullptr: ids / topk_w are inputs
+  int ldt, renorm;
+  int32_t *ids_out;        // routed ids / weights written back (logits != nullptr); ids_out may be nullptr
+  float *w_out;
+  int32_t *g1_done;        // per row block: GEMM1 tiles finished           } zero on entry,
+  int32_t *g1_seen;        // per row block: workgroups that saw them all   } zero again on exit
+  int32_t *bar;            // [0] arrived at / [1] left the barrier before the combine, [2] tokens routed
+  uint32_t *status;        // sticky error bits (kStatus*), or nullptr
 };
+
+// status bits a kernel sets when a bounded wait gives up (its output is then
+// not to be trusted); the host reads them with lq_moe_status
+constexpr uint32_t kStatusHandOver = 1u;   // a wave's hand-over of partial sums inside a workgroup
+constexpr uint32_t kStatusGemm1Wait = 2u;  // GEMM2 waiting for the GEMM1 tiles of its row block
+constexpr uint32_t kStatusGridWait = 4u;   // the fused kernel's barrier before the combine
+constexpr uint32_t kStatusRouteWait = 8u;  // the fused kernel waiting for the routing of every token
 
 // ---------------------------------------------------------------------------
 // weights -> MFMA B fragments (8 bf16 in K slot order [0,4,1,5,2,6,3,7])
@@ -178,6 +194,11 @@ __device__ __forceinline__ uint4 b_int8_exact(uint32_t d0, uint32_t d1, float s,
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// cache-policy operand of the raw buffer loads / stores: sc1 (agent scope) --
+// a load misses stale lines of this XCD's L2, a store writes through to the
+// agent's point of coherence
+constexpr int kCpolSc1 = 16;
 
 // raw buffer resource over [base, base + bytes) (gfx9 descriptor word 3);
 // loads at offsets >= bytes return zeros and touch no memory
@@ -915,8 +936,14 @@ template <int BITS, bool FIRST, bool G128>
 __global__ __launch_bounds__(kWThreads, 1) void moe_wide_kernel(MoeArgs a) {
   static_assert(kWT == 2, "G1 pairs the gate and up tile of each wave");
   __shared__ __align__(16) unsigned char lds[2 * kWStage];
-  __shared__ int r_asg[kWRows];    // G2: assignment and routing weight of each row of the item
-  __shared__ float r_wt[kWRows];
+  // G2: assignment and routing weight of each row of the item, two copies
+  // used by alternate items.  Item n's epilogue reads its copy after the
+  // item's last barrier; item n+1 writes the other copy in its prologue, and
+  // item n+2 -- the next writer of this copy -- starts only after every
+  // wave has passed item n+1's barriers, so no wave overwrites rows another
+  // wave still reads.
+  __shared__ int r_asg[2][kWRows];
+  __shared__ float r_wt[2][kWRows];
   const int nb = __builtin_amdgcn_readfirstlane(a.hdr->n_blk);
   const int ksplit = FIRST ? 1 : a.ksplit;
   const int per = (FIRST ? a.I / kWF1 : a.H / kWR2) * ksplit;  // items per block: slices x K slices
@@ -925,7 +952,8 @@ __global__ __launch_bounds__(kWThreads, 1) void moe_wide_kernel(MoeArgs a) {
   const int gx = gridDim.x >> 3;
   const int n8 = (n + 7) >> 3;
   const int end = min(n, (xcd + 1) * n8);
-  for (int t = xcd * n8 + static_cast<int>(blockIdx.x >> 3); t < end; t += gx) {
+  int parity = 0;
+  for (int t = xcd * n8 + static_cast<int>(blockIdx.x >> 3); t < end; t += gx, parity ^= 1) {
     const int blk = t / per;
     const int rem = t - blk * per;
     const int slice = rem / ksplit;
@@ -934,12 +962,14 @@ __global__ __launch_bounds__(kWThreads, 1) void moe_wide_kernel(MoeArgs a) {
     const int e = __builtin_amdgcn_readfirstlane(bi.x);
     const int row0 = __builtin_amdgcn_readfirstlane(bi.y);
     const int rows = __builtin_amdgcn_readfirstlane(bi.z);
+    int *ra = r_asg[parity];
+    float *rw = r_wt[parity];
     if (rows <= 32)
-      wide_item<BITS, 2, FIRST, G128>(a, e, slice, row0, rows, ks, lds, r_asg, r_wt);
+      wide_item<BITS, 2, FIRST, G128>(a, e, slice, row0, rows, ks, lds, ra, rw);
     else if (rows <= 64)
-      wide_item<BITS, 4, FIRST, G128>(a, e, slice, row0, rows, ks, lds, r_asg, r_wt);
+      wide_item<BITS, 4, FIRST, G128>(a, e, slice, row0, rows, ks, lds, ra, rw);
     else
-      wide_item<BITS, 8, FIRST, G128>(a, e, slice, row0, rows, ks, lds, r_asg, r_wt);
+      wide_item<BITS, 8, FIRST, G128>(a, e, slice, row0, rows, ks, lds, ra, rw);
   }
 }
 
@@ -1018,7 +1048,7 @@ constexpr int kSlotBytes = kRowsMax * 16 * 4;
 // of one block for the whole K, then the hand-over slots
 __host__ __device__ inline size_t stream_rows_bytes(int K) { return static_cast<size_t>(K) * kRowsMax * 2; }
 inline size_t stream_lds_bytes(int K) { return stream_rows_bytes(K) + static_cast<size_t>(kSWaves) * kSlotBytes; }
-// upper bound of the static LDS of the streaming kernels (block_plan's tables)
+// upper bound of the static LDS of the streaming and fused kernels
 constexpr size_t kStaticLds = 8192;
 
 
@@ -1026,10 +1056,13 @@ constexpr size_t kStaticLds = 8192;
 // G1 copies x into K-slot order; G2 builds act = SwiGLU(g, u) from
 // the gate / up pre-activations and permutes it into K-slot order.
 // A block of <= 32 rows with K <= 12 * 128 (G1) or 6 * 128 (G2) is one
-// batch of loads, all in flight at once.
-template <bool FIRST>
+// batch of loads, all in flight at once.  COH: the gate / up rows were
+// written by other workgroups of the same launch, so they are read with
+// agent-scope (sc1) loads, which do not hit stale lines of this XCD's L2.
+template <bool FIRST, bool COH = false>
 __device__ __forceinline__ void stage_block(const MoeArgs &a, int row0, int rows, const int32_t *rtok,
                                             unsigned char *lds) {
+  constexpr int kCpol = COH ? kCpolSc1 : 0;
   const int K = FIRST ? a.H : a.I;
   const int nk = K / kKC;
   const int per_row = nk * 16;  // 16-byte pieces (8 values) per row
@@ -1060,8 +1093,8 @@ __device__ __forceinline__ void stage_block(const MoeArgs &a, int row0, int rows
         v[i] = __builtin_amdgcn_raw_buffer_load_b128(src_rsrc, rtok[r] * (2 * a.H) + col, 0, 0);
       } else {
         const int off = r * (4 * a.I) + col;
-        v[i] = __builtin_amdgcn_raw_buffer_load_b128(src_rsrc, off, 0, 0);            // gate, 8 features
-        vu[i] = __builtin_amdgcn_raw_buffer_load_b128(src_rsrc, off + 2 * a.I, 0, 0);  // up, same features
+        v[i] = __builtin_amdgcn_raw_buffer_load_b128(src_rsrc, off, 0, kCpol);            // gate, 8 features
+        vu[i] = __builtin_amdgcn_raw_buffer_load_b128(src_rsrc, off + 2 * a.I, 0, kCpol);  // up, same features
       }
       dst[i] = q0i < total ? (c * kRowsMax + r) * kRowBytes + 16 * (pc ^ (r & 15)) : -1;
     }
@@ -1117,9 +1150,21 @@ __device__ __forceinline__ void run_steps(Step step) {
 // Otherwise wave w takes left-over unit t = w whole.  Per wave that makes up
 // to three segments of runs: the head (S1), the full rounds (S2, unit
 // stride W) and the left-over unit or tail (S3).
-template <int BITS, bool FOLDED, bool FIRST, int NRT, int KD, bool SQ>
+// COH (fused layer kernel): the epilogue stores are agent-scope (sc1), so
+// workgroups on other XCDs can read them in the same launch, and G2 stages
+// its rows with sc1 loads.  PRE: the wave's first run of codes is issued
+// before the staging, then hook() runs (every thread calls it; it may hold
+// barriers and the wait for the rows' producers), so the codes stream while
+// the workgroup waits.  rwt: routing weight of each row (G2), else
+// a.topk_w[rasg[m]].
+struct NoHook {
+  __device__ void operator()() const {}
+};
+template <int BITS, bool FOLDED, bool FIRST, int NRT, int KD, bool SQ, bool COH = false, bool PRE = false,
+          class Hook = NoHook>
 __device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, int rows, const int32_t *rtok,
-                                             const int32_t *rasg, int u_first, int u_end, unsigned char *lds) {
+                                             const int32_t *rasg, int u_first, int u_end, unsigned char *lds,
+                                             Hook hook = Hook{}, const float *rwt = nullptr) {
   __shared__ int hand_flag[kSWaves];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -1279,7 +1324,7 @@ __device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, 
       } else {
         const int asg = m < rows ? rasg[m] : 0;
         eoff[rt][j] = m < rows ? asg * ld + lc : -1;
-        ewt[rt][j] = m < rows ? a.topk_w[asg] : 0.0f;
+        ewt[rt][j] = m < rows ? (rwt ? rwt[m] : a.topk_w[asg]) : 0.0f;
       }
     }
   auto epilogue = [&](int u) __attribute__((always_inline)) {
@@ -1290,9 +1335,17 @@ __device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, 
         if (eoff[rt][j] >= 0) {
           if constexpr (FIRST) {
             // gate (u < I / 16) or up pre-activation, rounded to bf16 (RNE)
-            a.act[eoff[rt][j] + 16 * u] = static_cast<uint16_t>(cvt2(tot[rt][0][j], 0.0f));
+            const uint16_t h = static_cast<uint16_t>(cvt2(tot[rt][0][j], 0.0f));
+            if constexpr (COH)
+              __hip_atomic_store(a.act + eoff[rt][j] + 16 * u, h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else
+              a.act[eoff[rt][j] + 16 * u] = h;
           } else {
-            a.ybuf[eoff[rt][j] + 16 * u] = tot[rt][0][j] * ewt[rt][j];
+            const float y = tot[rt][0][j] * ewt[rt][j];
+            if constexpr (COH)
+              __hip_atomic_store(a.ybuf + eoff[rt][j] + 16 * u, y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else
+              a.ybuf[eoff[rt][j] + 16 * u] = y;
           }
         }
       }
@@ -1312,14 +1365,20 @@ __device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, 
     __hip_atomic_store(&hand_flag[wave], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
   };
   // continue from the head wave src handed over (it works that head before
-  // anything else, so the wait is short; the cap only bounds the loop)
+  // anything else, so the wait is short; the cap only bounds the loop, and
+  // running out of it marks the call's status: the sums are then wrong)
   auto take = [&](int src) __attribute__((always_inline)) {
+    bool got = false;
     for (int spin = 0; spin < (1 << 22); ++spin) {
       // (one wave-uniform decision, so the loop exit is uniform)
       const int f = __hip_atomic_load(&hand_flag[src], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
-      if (__builtin_amdgcn_readfirstlane(f) != 0) break;
+      if (__builtin_amdgcn_readfirstlane(f) != 0) {
+        got = true;
+        break;
+      }
       __builtin_amdgcn_s_sleep(2);
     }
+    if (!got && lane == 0 && a.status) atomicOr(a.status, kStatusHandOver);
     const float *slot = slots + src * (kSlotBytes / 4);
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt)
@@ -1331,24 +1390,39 @@ __device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, 
   // refills it with chunk d of the next run
   WChunk<BITS> wb[KD][1];
   float sb[KD][1];
-  // the block's token rows, then the first run of codes
-  __syncthreads();  // the previous block's rows and hand-over slots are no longer read
-  if (lane == 0) hand_flag[wave] = 0;
-  stage_block<FIRST>(a, row0, rows, rtok, lds);
-  __syncthreads();
-  if (nruns == 0) return;
-  // The first run's codes go out after the barrier: at the kernel's start
-  // every CU asks for a run per wave at once, and a wave waits at the issue
-  // of its loads until the memory system takes them -- so each wave starts
-  // computing as soon as its own loads are out, instead of all waves
-  // waiting for the slowest one's.
-  if constexpr (SQ) load_sq(sq_cur);
-  run_steps<KD>([&](auto d_tag) __attribute__((always_inline)) {
-    constexpr int d = decltype(d_tag)::value;
-    load_w(d_tag, wb[d], sb[d]);
-    __builtin_amdgcn_sched_barrier(0);
-  });
-  next_run();
+  auto first_run = [&]() __attribute__((always_inline)) {
+    if constexpr (SQ) load_sq(sq_cur);
+    run_steps<KD>([&](auto d_tag) __attribute__((always_inline)) {
+      constexpr int d = decltype(d_tag)::value;
+      load_w(d_tag, wb[d], sb[d]);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    next_run();
+  };
+  if constexpr (PRE) {
+    // the first run of codes (registers only) goes out first; the hook's
+    // barriers also order the previous phase's reads of the LDS rows and
+    // hand-over flags before the staging below overwrites them
+    if (nruns > 0) first_run();
+    hook();
+    if (lane == 0) hand_flag[wave] = 0;
+    stage_block<FIRST, COH>(a, row0, rows, rtok, lds);
+    __syncthreads();
+    if (nruns == 0) return;
+  } else {
+    // the block's token rows, then the first run of codes
+    __syncthreads();  // the previous block's rows and hand-over slots are no longer read
+    if (lane == 0) hand_flag[wave] = 0;
+    stage_block<FIRST, COH>(a, row0, rows, rtok, lds);
+    __syncthreads();
+    if (nruns == 0) return;
+    // The first run's codes go out after the barrier: at the kernel's start
+    // every CU asks for a run per wave at once, and a wave waits at the issue
+    // of its loads until the memory system takes them -- so each wave starts
+    // computing as soon as its own loads are out, instead of all waves
+    // waiting for the slowest one's.
+    first_run();
+  }
   // SQ: whether every scale of the current unit takes the fast dequant
   // (decided per unit, so a run is all fast or all exact-slow); scale slots
   // past the row's last group are not looked at
@@ -1369,7 +1443,7 @@ __device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, 
   // left in the segment, unit stride
   int cseg, cu, cc, cseg_left, cstride;
   enter(-1, cseg, cu, cc, cseg_left, cstride);
-  if (split && cseg == 2) take(t3);
+  if (split && cseg == 2 && cseg_left > 0) take(t3);
   for (int r = 0; r < nruns; ++r) {
     // the run's A addresses, computed once and kept opaque so every step
     // and row tile reaches its fragment through the instruction's
@@ -1435,13 +1509,17 @@ __device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, 
   }
 }
 
-template <int BITS, bool FOLDED, bool FIRST, int KD, bool SQ>
+template <int BITS, bool FOLDED, bool FIRST, int KD, bool SQ, bool COH = false, bool PRE = false,
+          class Hook = NoHook>
 __device__ __forceinline__ void stream_block(const MoeArgs &a, int e, int row0, int rows, const int32_t *rtok,
-                                             const int32_t *rasg, int u_first, int u_end, unsigned char *lds) {
+                                             const int32_t *rasg, int u_first, int u_end, unsigned char *lds,
+                                             Hook hook = Hook{}, const float *rwt = nullptr) {
   if (rows <= 16)
-    stream_units<BITS, FOLDED, FIRST, 1, KD, SQ>(a, e, row0, rows, rtok, rasg, u_first, u_end, lds);
+    stream_units<BITS, FOLDED, FIRST, 1, KD, SQ, COH, PRE>(a, e, row0, rows, rtok, rasg, u_first, u_end, lds, hook,
+                                                            rwt);
   else
-    stream_units<BITS, FOLDED, FIRST, 2, KD, SQ>(a, e, row0, rows, rtok, rasg, u_first, u_end, lds);
+    stream_units<BITS, FOLDED, FIRST, 2, KD, SQ, COH, PRE>(a, e, row0, rows, rtok, rasg, u_first, u_end, lds, hook,
+                                                            rwt);
 }
 
 // Workgroup g of a grid of G runs on XCD g % 8.  Its XCD-major slot
@@ -1469,6 +1547,8 @@ __device__ __forceinline__ bool cu_share(int c, int G, int nb, int upb, int &b, 
   return true;
 }
 
+constexpr int kPlanMaxN = 2048;  // assignments the fused kernel plans (one workgroup)
+
 // Small layers (T*k <= kPlanMaxN): every workgroup derives the plan of its
 // own block from the T*k routed ids instead of reading plan_kernel's
 // output -- the same per-expert counts and offsets, the same expert-major
@@ -1480,7 +1560,6 @@ __device__ __forceinline__ bool cu_share(int c, int G, int nb, int upb, int &b, 
 // opens the staging orders those writes before any read).  Fills rtok / rasg
 // (token and assignment of each row) and returns false when the CU has no
 // block.
-constexpr int kPlanMaxN = 2048;
 __device__ __forceinline__ bool block_plan(const MoeArgs &a, int upb, int &e, int &row0, int &rows, int &ub,
                                            int &ue, int &im, int32_t *rtok, int32_t *rasg) {
   __shared__ int cnt[kMaxExperts];
@@ -1625,6 +1704,336 @@ __global__ __launch_bounds__(kSThreads, 1) void moe_stream_kernel(MoeArgs a) {
       const int b1 = static_cast<int>(static_cast<int64_t>(c + 1) * nb / G);
       for (int b = b0; b < b1; ++b) run_block(b, 0, upb);
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// fused layer kernel (the weight-bandwidth regime: E <= 64, T*k <= kPlanMaxN)
+//
+// One launch per layer: [route] -> plan -> G1 -> G2 -> combine, one 12-wave
+// workgroup per CU.  With logits, workgroup t < T routes token t (the router
+// kernel's arithmetic) and publishes its ids and weights; every workgroup then
+// derives the whole plan (counts, blocks of <= 32 rows, stable order) in one
+// wave, lane e = expert e, and takes a cost-weighted share of one row block in
+// each phase (assign_share: blocks of 17..32 rows run two row tiles and get
+// more CUs).  Workgroups exchange data three times:
+//   routing -> plan: the ids / weights of every token; each routing wave
+//     counts once on bar[2] when its stores are complete, and the plan starts
+//     when the count reaches T.
+//   G1 -> G2: the bf16 gate / up pre-activations of a row block, written by
+//     the workgroups whose G1 share is that block and read, all of them, by
+//     those whose G2 share is.  Each workgroup adds its G1 tile count to
+//     g1_done[b] once its stores are complete; G2 issues its first run of W2
+//     codes, then waits (bounded) for its block's count to reach 2I/16 before
+//     staging the rows.
+//   G2 -> combine: y of each assignment.  After a grid barrier (every
+//     workgroup's G2 stores complete), workgroup c sums slice c of the
+//     outputs: out[t, h] = bf16(sum_j y[t*k + j, h]) over the valid slots, j
+//     ascending -- combine_kernel's arithmetic, spread evenly over the grid.
+//     (Letting the last workgroup to finish a token's tiles combine it costs
+//     more: a late workgroup is last for all the tokens of its rows and
+//     combines them one after another.)
+// Visibility across XCDs without writing back or invalidating whole L2s:
+// the data goes out with agent-scope (sc1) stores, which write through to the
+// point of coherence, and is read with sc1 loads, which do not hit stale L2
+// lines.  Each wave waits for its stores (s_waitcnt vmcnt(0)) before the
+// workgroup barrier after which one thread adds to a counter; the counters
+// are agent-scope atomics.
+// The counters are zero on entry and left at zero: the last of a G2 block's
+// workgroups to see its G1 count (g1_seen) clears both, and the last
+// workgroup to leave the barrier clears its two counts and the routing count.
+// The waits need every workgroup resident at once: the grid is one
+// workgroup per CU (a second one fits on a CU only for small K, and then the
+// grid still fits).  A wait that runs out of its cap sets a status bit and
+// goes on (wrong output, no hang).
+// ---------------------------------------------------------------------------
+constexpr int kFusedRouteMaxT = 64;  // routing in the fused kernel up to this many tokens (E <= 64)
+constexpr int kWaitCap = 1 << 20;    // polls of a cross-workgroup wait (~1 s)
+
+// One phase's share of this workgroup in the fused kernel: row block b (its
+// index among the layer's blocks), the block's expert e and sorted rows
+// [row0, row0 + rows), j the block's place among its expert's blocks, and
+// the workgroup's tiles [ub, ue) of the block's upb, being the i-th of the
+// block's m workgroups.
+struct Share {
+  int b, e, j, row0, rows, ub, ue, i, m;
+};
+
+// Cost-weighted assignment of CU slot c (of G) to a row block, for E <= 64
+// with lane e = expert e holding its count cnt, block count nbk, and the
+// exclusive prefixes of both.  A block weighs wlo (<= 16 rows: one row tile
+// per weight tile) or whi (17..32 rows: two); the blocks, expert-major, share
+// the G slots in proportion to their weights: block [S, S + w) of the total
+// W covers slots [ceil(S G / W), ceil((S + w) G / W)).  Every block gets at
+// least one slot when W <= wlo G (host-checked through the block count).
+__device__ __forceinline__ Share assign_share(int c, int G, int cnt, int nbk, int bexcl, int cexcl, int wlo, int whi,
+                                              int upb) {
+  auto wrows = [&](int r) { return r > 16 ? whi : wlo; };
+  const int w32 = wrows(kRowsMax);
+  const int we = nbk > 0 ? (nbk - 1) * w32 + wrows(cnt - kRowsMax * (nbk - 1)) : 0;
+  const int pinc = wave_incl_scan(we);
+  const int W = __builtin_amdgcn_readlane(pinc, 63);
+  const int pex = pinc - we;
+  // the expert: the highest one with blocks whose weight starts at or before c W / G
+  const uint64_t own = __ballot(nbk > 0 && pex * G <= c * W);
+  Share sh;
+  sh.e = 63 - __builtin_clzll(own);
+  const int pe = __builtin_amdgcn_readlane(pex, sh.e);
+  const int ne = __builtin_amdgcn_readlane(nbk, sh.e);
+  const int ce = __builtin_amdgcn_readlane(cnt, sh.e);
+  sh.j = min((c * W - pe * G) / (w32 * G), ne - 1);
+  sh.rows = min(kRowsMax, ce - kRowsMax * sh.j);
+  const int S = pe + sh.j * w32, S2 = S + wrows(sh.rows);
+  const int first = (S * G + W - 1) / W, next = (S2 * G + W - 1) / W;
+  sh.b = __builtin_amdgcn_readlane(bexcl, sh.e) + sh.j;
+  sh.row0 = __builtin_amdgcn_readlane(cexcl, sh.e) + kRowsMax * sh.j;
+  sh.m = next - first;
+  sh.i = c - first;
+  sh.ub = sh.i * upb / sh.m;
+  sh.ue = (sh.i + 1) * upb / sh.m;
+  return sh;
+}
+
+// cost weights of a block (<= 16 rows, 17..32 rows) per phase, measured on
+// MI355X at C4: GEMM1's two-row-tile blocks take ~1.1x as long, GEMM2's
+// ~1.8x (its K is half as long, so the per-row costs of staging the SwiGLU
+// rows and of the row tiles' MFMAs weigh more)
+constexpr int kW1Lo = 10, kW1Hi = 11, kW2Lo = 5, kW2Hi = 9;
+
+// One wave: the assignments of expert e with ranks [first, first + rows) among
+// its assignments in ascending flat index, from ids_l (the expert of each of
+// the N assignments, 0xFFFF for none): token -> tok[r], assignment -> asg[r]
+// (either may be null).
+__device__ __forceinline__ void compact_rows(const uint16_t *ids_l, int N, int k, int e, int first, int rows,
+                                             int32_t *tok, int32_t *asg) {
+  const int lane = threadIdx.x & 63;
+  const unsigned long long lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  const int last = first + rows;
+  int run = 0;
+  for (int c0 = 0; c0 < N && run < last; c0 += 64) {
+    const int i = c0 + lane;
+    const bool hit = i < N && ids_l[i] == e;
+    const unsigned long long bal = __ballot(hit);
+    const int rank = run + __popcll(bal & lt);
+    if (hit && rank >= first && rank < last) {
+      if (tok) tok[rank - first] = i / k;
+      if (asg) asg[rank - first] = i;
+    }
+    run += __popcll(bal);
+  }
+}
+
+// Slice blockIdx.x of the layer's combine: out[t, h..h+4) = bf16(sum_j y[t*k +
+// j, h..h+4)) over the slots with a valid id, j ascending (combine_kernel's
+// sums), y read with sc1 loads (other workgroups wrote it in this launch).
+// Slots without a valid id were never written and are left out; with routing
+// in-kernel every id is valid.
+__device__ __forceinline__ void fused_combine(const MoeArgs &a, bool route) {
+  const int k = a.k, H = a.H;
+  const int64_t nq = a.T * H / 4;  // 4 outputs per task
+  const int64_t q0 = nq * blockIdx.x / gridDim.x, q1 = nq * (blockIdx.x + 1) / gridDim.x;
+  // (the host bounds T*k*H*4 below 2^31: 32-bit byte offsets)
+  const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.ybuf, a.T * k * H * 4);
+  for (int64_t q = q0 + threadIdx.x; q < q1; q += kSThreads) {
+    const int64_t t = q / (H / 4);
+    const int h = static_cast<int>(q - t * (H / 4)) * 4;
+    floatx4 s = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j0 = 0; j0 < k; j0 += 8) {
+      // up to 8 slots' loads in flight at once; slots past k or without a
+      // valid id read the token's first slot and are not added
+      floatx4 v[8];
+      bool ok[8];
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const int j = j0 + jj;
+        const int id = j < k ? (route ? 0 : a.ids[t * k + j]) : -1;
+        ok[jj] = id >= 0 && id < a.E;
+        const int off = static_cast<int>(((t * k + (ok[jj] ? j : 0)) * H + h) * 4);
+        v[jj] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(yr, off, 0, kCpolSc1));
+      }
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj)
+        if (ok[jj]) s += v[jj];
+    }
+    uint2 o;
+    o.x = static_cast<uint32_t>(f32_to_bf16_bits(s[0])) | (static_cast<uint32_t>(f32_to_bf16_bits(s[1])) << 16);
+    o.y = static_cast<uint32_t>(f32_to_bf16_bits(s[2])) | (static_cast<uint32_t>(f32_to_bf16_bits(s[3])) << 16);
+    *reinterpret_cast<uint2 *>(a.out + t * H + h) = o;
+  }
+}
+
+// the plan's tables fit the smallest rows area (K = 512)
+constexpr int kPlanLds = 2 * kPlanMaxN + 64 * 8 + kFusedRouteMaxT * 64 + 64 * 4;
+static_assert(kPlanLds <= 512 * kRowsMax * 2, "plan tables exceed the rows area");
+
+// Route token t (logits row t, E <= 64, lane e = expert e) with one wave:
+// ids and weights to slots t*k + rank of ids_out / w_out with agent-scope
+// stores, then, once they are complete, one count on route_cnt.
+__device__ __forceinline__ void fused_route_token(const MoeArgs &a, int t) {
+  const int lane = threadIdx.x & 63;
+  const int E = a.E, k = a.k;
+  const int64_t idx = static_cast<int64_t>(t) * E + min(lane, E - 1);
+  float v = a.ldt == LQ_F32 ? load_f32<LQ_F32>(a.logits, idx)
+                            : a.ldt == LQ_F16 ? load_f32<LQ_F16>(a.logits, idx) : load_f32<LQ_BF16>(a.logits, idx);
+  if (lane >= E) v = -__builtin_inff();
+  route_values64(v, E, k, a.renorm, [&](int rank, int e, float w) __attribute__((always_inline)) {
+    __hip_atomic_store(a.ids_out + t * k + rank, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.w_out + t * k + rank, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  });
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's id / weight stores are complete
+  if (lane == 0) __hip_atomic_fetch_add(a.bar + 2, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int BITS, int KD1, int KD2, bool SQ>
+__global__ __launch_bounds__(kSThreads, 1) void moe_fused_kernel(MoeArgs a) {
+  extern __shared__ __align__(16) unsigned char slds[];
+  __shared__ int32_t rtok[kRowsMax], rasg[kRowsMax];
+  __shared__ float rwt[kRowsMax];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int N = static_cast<int>(a.T * a.k);
+  const int T = static_cast<int>(a.T), k = a.k, H = a.H, E = a.E;
+  const int G = gridDim.x, c = xcd_slot(blockIdx.x, gridDim.x);
+  const bool route = a.logits != nullptr;
+  // plan tables, in the rows area until the G1 staging: the expert of each
+  // assignment (ids given), or each expert's token mask and each (token,
+  // expert) pair's slot (routing in-kernel); the expert counts
+  uint16_t *ids_l = reinterpret_cast<uint16_t *>(slds);
+  unsigned long long *mask_l = reinterpret_cast<unsigned long long *>(slds + 2 * kPlanMaxN);
+  uint8_t *slot_l = slds + 2 * kPlanMaxN + 64 * 8;
+  int *cnt_l = reinterpret_cast<int *>(slds + 2 * kPlanMaxN + 64 * 8 + kFusedRouteMaxT * 64);
+
+  // ---- routing (workgroup t < T routes token t) and the expert counts
+  if (tid < 64) {
+    cnt_l[tid] = 0;
+    mask_l[tid] = 0;
+  }
+  if (route) {
+    if (wave == 0 && static_cast<int>(blockIdx.x) < T) fused_route_token(a, blockIdx.x);
+    if (tid == 0) {
+      bool ok = false;
+      for (int spin = 0; spin < kWaitCap; ++spin) {
+        if (__hip_atomic_load(a.bar + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= T) {
+          ok = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      if (!ok && a.status) atomicOr(a.status, kStatusRouteWait);
+    }
+    __syncthreads();
+    for (int i = tid; i < N; i += kSThreads) {
+      const int id = __hip_atomic_load(a.ids_out + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int t = i / k;
+      atomicOr(mask_l + id, 1ull << t);
+      slot_l[t * 64 + id] = static_cast<uint8_t>(i - t * k);
+    }
+  } else {
+    __syncthreads();
+    for (int i = tid; i < N; i += kSThreads) {
+      const int id = a.ids[i];
+      const bool ok = id >= 0 && id < E;
+      ids_l[i] = ok ? static_cast<uint16_t>(id) : uint16_t{0xFFFF};
+      if (ok) atomicAdd(cnt_l + id, 1);
+    }
+  }
+  __syncthreads();
+  const unsigned long long mask = route ? mask_l[lane] : 0ull;
+  const int cnt = route ? __popcll(mask) : (lane < E ? cnt_l[lane] : 0);
+
+  // ---- the plan: blocks of <= 32 rows, expert-major; this workgroup's share of each phase
+  const int nbk = (cnt + kRowsMax - 1) / kRowsMax;
+  const int cinc = wave_incl_scan(cnt), binc = wave_incl_scan(nbk);
+  if (__builtin_amdgcn_readlane(binc, 63) == 0) {
+    // no valid assignment (ids given): every output is zero
+    fused_combine(a, route);
+    return;
+  }
+  const int upb1 = 2 * a.I / 16, upb2 = H / 16;
+  const Share s1 = assign_share(c, G, cnt, nbk, binc - nbk, cinc - cnt, kW1Lo, kW1Hi, upb1);
+  const Share s2 = assign_share(c, G, cnt, nbk, binc - nbk, cinc - cnt, kW2Lo, kW2Hi, upb2);
+  // rows: wave 0 the tokens of the G1 block, wave 1 the assignments and routing weights of the G2 block
+  if (wave < 2) {
+    const Share &sh = wave == 0 ? s1 : s2;
+    if (route) {
+      const unsigned long long me =
+          (static_cast<unsigned long long>(static_cast<uint32_t>(__builtin_amdgcn_readlane(
+               static_cast<int>(mask >> 32), sh.e))) << 32) |
+          static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(mask & 0xFFFFFFFFu), sh.e));
+      const unsigned long long below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+      const int r = __popcll(me & below) - kRowsMax * sh.j;
+      if (((me >> lane) & 1) && r >= 0 && r < sh.rows) {
+        if (wave == 0) {
+          rtok[r] = lane;
+        } else {
+          const int asg = lane * k + slot_l[lane * 64 + sh.e];
+          rasg[r] = asg;
+          rwt[r] = __hip_atomic_load(a.w_out + asg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    } else {
+      compact_rows(ids_l, N, k, sh.e, kRowsMax * sh.j, sh.rows, wave == 0 ? rtok : nullptr,
+                   wave == 0 ? nullptr : rasg);
+      if (wave == 1 && lane < sh.rows) rwt[lane] = a.topk_w[rasg[lane]];
+    }
+  }
+  __syncthreads();  // rows complete; the plan tables are no longer read (the G1 staging overwrites them)
+
+  // ---- G1: this workgroup's share of its G1 block's W1 tiles
+  stream_block<BITS, false, true, KD1, SQ, true>(a, s1.e, s1.row0, s1.rows, rtok, nullptr, s1.ub, s1.ue, slds);
+  __builtin_amdgcn_s_waitcnt(0);  // every gate / up store of this wave is complete
+
+  // ---- G2: this workgroup's share of its G2 block's W2 tiles, once that block's G1 is complete
+  int seen = 0;
+  auto wait_g1 = [&]() __attribute__((always_inline)) {
+    __syncthreads();  // every wave's G1 stores are complete
+    if (tid == 0) {
+      __hip_atomic_fetch_add(a.g1_done + s1.b, s1.ue - s1.ub, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      bool ok = false;
+      for (int spin = 0; spin < kWaitCap; ++spin) {
+        if (__hip_atomic_load(a.g1_done + s2.b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= upb1) {
+          ok = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      if (!ok && a.status) atomicOr(a.status, kStatusGemm1Wait);
+      seen = __hip_atomic_fetch_add(a.g1_seen + s2.b, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+  };
+  stream_block<BITS, false, false, KD2, SQ, true, true>(a, s2.e, s2.row0, s2.rows, nullptr, rasg, s2.ub, s2.ue, slds,
+                                                         wait_g1, rwt);
+  __builtin_amdgcn_s_waitcnt(0);  // every y store of this wave is complete
+  __syncthreads();
+  int left = 0;
+  if (tid == 0) {
+    __hip_atomic_fetch_add(a.bar, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bool ok = false;
+    for (int spin = 0; spin < kWaitCap; ++spin) {
+      if (__hip_atomic_load(a.bar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= static_cast<int>(gridDim.x)) {
+        ok = true;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (!ok && a.status) atomicOr(a.status, kStatusGridWait);
+    left = __hip_atomic_fetch_add(a.bar + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  fused_combine(a, route);
+  if (tid == 0 && left == static_cast<int>(gridDim.x) - 1) {
+    // every workgroup has passed the barrier (and long since the routing
+    // count): clear them for the next call
+    __hip_atomic_store(a.bar, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.bar + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.bar + 2, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (tid == 0 && seen == s2.m - 1) {
+    // every workgroup of the G2 block has seen its G1 count: clear it for the next call
+    __hip_atomic_store(a.g1_done + s2.b, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.g1_seen + s2.b, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -1888,6 +2297,7 @@ __global__ __launch_bounds__(256) void linear_setup_kernel(const uint16_t *__res
 // ---------------------------------------------------------------------------
 
 struct WsLayout {
+  size_t status, g1_done, g1_seen, bar, sync_end;  // sync region: zero before the first call, left zero
   size_t counts, offsets, sorted, srow, hdr, blocks, slotplan, slotasg, segcnt, ids, weights, xperm, act, ybuf, total;
 };
 
@@ -1902,6 +2312,13 @@ int64_t max_blocks_for(int64_t T, int E, int k) {
   return std::min<int64_t>(E, N) + N / kRowsMax;
 }
 
+// The workspace starts with the sync region -- the status word (at offset
+// 0) and the fused kernel's counters (per row block, up to kSyncBlocks of
+// them, and its grid barrier) -- which must be zero before the first call on a
+// workspace (lq_moe_workspace_init) and which every call leaves zero.  Its
+// size and place do not depend on the shape, so one initialisation serves
+// every later call.  The rest is scratch each call overwrites.
+constexpr int kSyncBlocks = 1024;  // CUs the fused kernel's per-block counters cover
 WsLayout ws_layout(int64_t T, int H, int I, int E, int k) {
   const int64_t N = T * k;
   WsLayout w;
@@ -1910,6 +2327,11 @@ WsLayout ws_layout(int64_t T, int H, int I, int E, int k) {
     field = off;
     off = align256(off + bytes);
   };
+  take(w.status, sizeof(uint32_t));
+  take(w.g1_done, sizeof(int32_t) * kSyncBlocks);
+  take(w.g1_seen, sizeof(int32_t) * kSyncBlocks);
+  take(w.bar, sizeof(int32_t) * 4);
+  w.sync_end = off;
   take(w.counts, sizeof(int32_t) * E);
   take(w.offsets, sizeof(int32_t) * (E + 1));
   take(w.sorted, sizeof(int32_t) * N);
@@ -1996,7 +2418,8 @@ int validate_layer(const void *x, int64_t T, int H, int I, int E, int k, const i
   if (E < 1 || E > kMaxExperts)
     return fail(LQ_ERR_UNSUPPORTED, "moe_forward: 1 <= num_experts <= " + std::to_string(kMaxExperts));
   if (k > E) return fail(LQ_ERR_VALUE, "moe_forward: top_k exceeds num_experts");
-  if (flags & ~(LQ_MOE_FOLDED_SCALES | LQ_MOE_GENERAL_KERNEL | LQ_MOE_WIDE_KERNEL | LQ_MOE_STREAM_KERNEL))
+  if (flags & ~(LQ_MOE_FOLDED_SCALES | LQ_MOE_GENERAL_KERNEL | LQ_MOE_WIDE_KERNEL | LQ_MOE_STREAM_KERNEL |
+                LQ_MOE_FUSED_LAYER))
     return fail(LQ_ERR_VALUE, "moe_forward: unknown flags");
   {
     const int forced = flags & (LQ_MOE_GENERAL_KERNEL | LQ_MOE_WIDE_KERNEL | LQ_MOE_STREAM_KERNEL);
@@ -2075,24 +2498,29 @@ bool stream_eligible(int bits, int H, int I, int64_t g1, int64_t g2) {
          lds + kStaticLds <= static_cast<size_t>(device_info().max_lds);
 }
 
+// let a kernel's dynamic LDS take what its static LDS leaves of the
+// workgroup's share (once per kernel and process)
+template <class Fn>
+int allow_dynamic_lds(Fn *fn, std::once_flag &once, hipError_t &rc) {
+  std::call_once(once, [&] {
+    hipFuncAttributes fa{};
+    rc = hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(fn));
+    if (rc == hipSuccess)
+      rc = hipFuncSetAttribute(reinterpret_cast<const void *>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               device_info().max_lds - static_cast<int>(fa.sharedSizeBytes));
+  });
+  if (rc != hipSuccess) return fail(LQ_ERR_RUNTIME, std::string("hipFuncSetAttribute failed: ") + hipGetErrorString(rc));
+  return LQ_OK;
+}
+
 template <int BITS, bool FOLDED, bool FIRST, int KD, bool SQ, int PLAN>
 int launch_stream_kd(const MoeArgs &a, hipStream_t st) {
-  const DeviceInfo dev = device_info();
-  static std::once_flag attr_once;
+  static std::once_flag once;
   static hipError_t attr_rc = hipSuccess;
-  std::call_once(attr_once, [&] {
-    // dynamic LDS may take what the kernel's static LDS leaves
-    const void *fn = reinterpret_cast<const void *>(moe_stream_kernel<BITS, FOLDED, FIRST, KD, SQ, PLAN>);
-    hipFuncAttributes fa{};
-    attr_rc = hipFuncGetAttributes(&fa, fn);
-    if (attr_rc == hipSuccess)
-      attr_rc = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    dev.max_lds - static_cast<int>(fa.sharedSizeBytes));
-  });
-  if (attr_rc != hipSuccess)
-    return fail(LQ_ERR_RUNTIME, std::string("hipFuncSetAttribute failed: ") + hipGetErrorString(attr_rc));
+  const int rc = allow_dynamic_lds(moe_stream_kernel<BITS, FOLDED, FIRST, KD, SQ, PLAN>, once, attr_rc);
+  if (rc) return rc;
   const size_t lds = stream_lds_bytes(FIRST ? a.H : a.I);
-  moe_stream_kernel<BITS, FOLDED, FIRST, KD, SQ, PLAN><<<dev.cus, kSThreads, lds, st>>>(a);
+  moe_stream_kernel<BITS, FOLDED, FIRST, KD, SQ, PLAN><<<device_info().cus, kSThreads, lds, st>>>(a);
   return check_launch(FIRST ? "moe_stream_gemm1" : "moe_stream_gemm2");
 }
 
@@ -2104,27 +2532,63 @@ int launch_stream_plan(const MoeArgs &a, hipStream_t st, bool inplan) {
   return launch_stream_kd<BITS, FOLDED, FIRST, KD, SQ, FIRST ? kPlanOwn : kPlanSlot>(a, st);
 }
 
-// chunks in flight per wave: 8 KB of codes where K allows (INT4: 8 x 1 KB,
-// INT8: 4 x 2 KB), half that otherwise; the folded INT4 form keeps 4 (its
-// extra accumulators leave no registers for 8).  The exact INT4 form also
-// takes 4 when 8 would leave an odd number of runs per unit: left-over
-// units are then split between waves, which gains more than the deeper
-// prefetch (a unit of 8 chunks: 23.4 us instead of 24.7 us for the C4
-// down projection).  inplan: the kernels plan their blocks themselves
-// (small layers; no plan_kernel ran).
+// chunks in flight per wave for reduction length nk * 128: 8 KB of codes
+// where K allows (INT4: 8 x 1 KB, INT8: 4 x 2 KB), half that otherwise; the
+// folded INT4 form keeps 4 (its extra accumulators leave no registers for
+// 8).  The exact INT4 form also takes 4 when 8 would leave an odd number of
+// runs per unit: left-over units are then split between waves, which gains
+// more than the deeper prefetch (a unit of 8 chunks: 23.4 us instead of
+// 24.7 us for the C4 down projection).
+template <int BITS, bool FOLDED>
+int stream_kd(int nk) {
+  constexpr int kDeep = BITS == 4 ? (FOLDED ? 4 : 8) : 4;
+  return nk % kDeep == 0 && (kDeep < 8 || (nk / kDeep) % 2 == 0) ? kDeep : kDeep / 2;
+}
+
+// per-unit scale loads (SQ): group length 128, at most 16 groups, runs of at least 4 chunks
+inline bool stream_sq(int group, int nk, int kd) { return group == kKC && nk <= 16 && kd >= 4; }
+
 template <int BITS, bool FOLDED, bool FIRST>
 int launch_stream(const MoeArgs &a, hipStream_t st, bool inplan) {
   const int nk = (FIRST ? a.H : a.I) / kKC;
   constexpr int kDeep = BITS == 4 ? (FOLDED ? 4 : 8) : 4;
-  // per-unit scale loads: group length 128, at most 16 groups, runs of 4
-  const bool sq = (FIRST ? a.g1 : a.g2) == kKC && nk <= 16;
-  if (nk % kDeep == 0 && (kDeep < 8 || (nk / kDeep) % 2 == 0))
+  const int kd = stream_kd<BITS, FOLDED>(nk);
+  const bool sq = stream_sq(FIRST ? a.g1 : a.g2, nk, kd);
+  if (kd == kDeep)
     return sq ? launch_stream_plan<BITS, FOLDED, FIRST, kDeep, true>(a, st, inplan)
               : launch_stream_plan<BITS, FOLDED, FIRST, kDeep, false>(a, st, inplan);
   if constexpr (kDeep / 2 >= 4) {
     if (sq) return launch_stream_plan<BITS, FOLDED, FIRST, kDeep / 2, true>(a, st, inplan);
   }
   return launch_stream_plan<BITS, FOLDED, FIRST, kDeep / 2, false>(a, st, inplan);
+}
+
+template <int BITS, int KD1, int KD2, bool SQ>
+int launch_fused_k(const MoeArgs &a, hipStream_t st) {
+  static std::once_flag once;
+  static hipError_t attr_rc = hipSuccess;
+  const int rc = allow_dynamic_lds(moe_fused_kernel<BITS, KD1, KD2, SQ>, once, attr_rc);
+  if (rc) return rc;
+  const size_t lds = stream_lds_bytes(std::max(a.H, a.I));
+  moe_fused_kernel<BITS, KD1, KD2, SQ><<<device_info().cus, kSThreads, lds, st>>>(a);
+  return check_launch("moe_fused_layer");
+}
+
+// the fused layer kernel with each GEMM's run depth; per-unit scale loads
+// when both GEMMs can take them
+template <int BITS>
+int launch_fused(const MoeArgs &a, hipStream_t st) {
+  constexpr int kHi = BITS == 4 ? 8 : 4, kLo = kHi / 2;
+  const int nk1 = a.H / kKC, nk2 = a.I / kKC;
+  const int kd1 = stream_kd<BITS, false>(nk1), kd2 = stream_kd<BITS, false>(nk2);
+  const bool sq = stream_sq(a.g1, nk1, kd1) && stream_sq(a.g2, nk2, kd2);
+  if (kd1 == kHi && kd2 == kHi)
+    return sq ? launch_fused_k<BITS, kHi, kHi, true>(a, st) : launch_fused_k<BITS, kHi, kHi, false>(a, st);
+  if (kd1 == kHi)
+    return sq && kLo >= 4 ? launch_fused_k<BITS, kHi, kLo, kLo >= 4>(a, st) : launch_fused_k<BITS, kHi, kLo, false>(a, st);
+  if (kd2 == kHi)
+    return sq && kLo >= 4 ? launch_fused_k<BITS, kLo, kHi, kLo >= 4>(a, st) : launch_fused_k<BITS, kLo, kHi, false>(a, st);
+  return sq && kLo >= 4 ? launch_fused_k<BITS, kLo, kLo, kLo >= 4>(a, st) : launch_fused_k<BITS, kLo, kLo, false>(a, st);
 }
 
 template <int BITS, bool FOLDED>
@@ -2246,57 +2710,29 @@ Path choose_path(int bits, int64_t T, int H, int I, int E, int k, int64_t group_
   return Path::kGeneral;
 }
 
-// [x permute] -> [plan] -> G1 -> G2 -> combine.  The streaming GEMMs stage
-// x itself; the general ones need its K-slot permuted copy in the workspace
-// (x_permuted: already written by the router).
-int moe_forward_impl(const void *x, bool x_permuted, int64_t T, int H, int I, int E, int k,
-                     const int8_t *q1, const float *s1, const int8_t *q2, const float *s2, int bits,
-                     int64_t group_w1, int64_t group_w2, int flags, const int32_t *topk_ids,
-                     const float *topk_weights, char *ws, void *out, hipStream_t st, ProfileMarks &pm,
-                     int first_mark) {
-  const WsLayout w = ws_layout(T, H, I, E, k);
-  const int64_t g1 = effective_group(H, group_w1);
-  const int64_t g2 = effective_group(I, group_w2);
-  // the folded form applies one scale per 128-wide K chunk
-  const bool folded = (flags & LQ_MOE_FOLDED_SCALES) && g1 % kKC == 0 && g2 % kKC == 0;
-  const Path path = choose_path(bits, T, H, I, E, k, group_w1, group_w2, flags);
-  const bool stream = path == Path::kStream;
-
-  PlanArgs p = plan_args(topk_ids, T, E, k, ws, w);
-  if (path == Path::kWide) p.block_rows = kWRows;
-  uint16_t *xperm = reinterpret_cast<uint16_t *>(ws + w.xperm);
-  if (!stream && !x_permuted) {
-    const int64_t n8 = T * H / 8;
-    permute_rows_kernel<<<static_cast<int>(ceil_div(n8, 256)), 256, 0, st>>>(static_cast<const uint16_t *>(x), n8,
-                                                                             xperm);
-  }
-  // small layers on the streaming GEMMs plan their blocks in-kernel
-  // (every block of the in-kernel plan needs a CU of its own: there are at
-  // most ceil(T*k / 32) + min(E, T*k) blocks)
+// The fused layer kernel takes a streaming-family layer whose assignments one
+// workgroup plans (T*k <= kPlanMaxN) and whose row blocks each get a CU of
+// their own (at most ceil(T*k / 32) + min(E, T*k) blocks), in the exact
+// weight form.
+bool fused_eligible(Path path, bool folded, int64_t T, int E, int k, int flags) {
+  if (!(flags & LQ_MOE_FUSED_LAYER)) return false;
   const int64_t nb_max = ceil_div(T * k, kRowsMax) + std::min<int64_t>(E, T * k);
-  const bool inplan =
-      stream && T * k <= kPlanMaxN && nb_max <= device_info().cus && device_info().cus <= kMaxSlots;
-  int rc = LQ_OK;
-  if (!inplan) {
-    const int64_t nseg = ceil_div(T * k, kPlanSeg);
-    if (nseg > 1) {  // large layers: one workgroup per segment of assignments
-      int32_t *segcnt = reinterpret_cast<int32_t *>(ws + w.segcnt);
-      plan_count_kernel<<<static_cast<int>(nseg), kPlanBlock, 0, st>>>(p, segcnt);
-      rc = check_launch("moe_plan_count");
-      if (rc) return rc;
-      plan_scatter_kernel<<<static_cast<int>(nseg), kPlanBlock, 0, st>>>(p, segcnt, static_cast<int>(nseg));
-      rc = check_launch("moe_plan_scatter");
-    } else {
-      plan_kernel<<<1, kPlanBlock, 0, st>>>(p);
-      rc = check_launch("moe_plan");
-    }
-    if (rc) return rc;
-  }
-  pm.mark(first_mark);
+  const int64_t cus = device_info().cus;
+  // every block gets a CU in both phases' cost-weighted splits
+  const bool fits = nb_max * kW1Hi <= kW1Lo * cus && nb_max * kW2Hi <= kW2Lo * cus;
+  return path == Path::kStream && !folded && E <= 64 && T * k <= kPlanMaxN && fits && cus <= kSyncBlocks;
+}
 
-  MoeArgs a;
+// Routing inside the fused kernel: workgroup t routes token t (one wave, E <= 64).
+bool route_in_kernel(int64_t T, int E) { return T <= kFusedRouteMaxT && T <= device_info().cus && E <= 64; }
+
+// Layer arguments over the workspace and the caller's buffers.
+MoeArgs layer_args(const void *x, int64_t T, int H, int I, int E, int k, const int8_t *q1, const float *s1,
+                   const int8_t *q2, const float *s2, int64_t g1, int64_t g2, const int32_t *topk_ids,
+                   const float *topk_weights, char *ws, const WsLayout &w, const PlanArgs &p, void *out) {
+  MoeArgs a{};
   a.x = static_cast<const uint16_t *>(x);
-  a.xperm = xperm;
+  a.xperm = reinterpret_cast<uint16_t *>(ws + w.xperm);
   a.q1 = q1;
   a.s1 = s1;
   a.q2 = q2;
@@ -2323,6 +2759,80 @@ int moe_forward_impl(const void *x, bool x_permuted, int64_t T, int H, int I, in
   a.g2 = static_cast<int>(g2);
   a.ng2 = static_cast<int>(I / g2);
   a.ksplit = 1;
+  a.g1_done = reinterpret_cast<int32_t *>(ws + w.g1_done);
+  a.g1_seen = reinterpret_cast<int32_t *>(ws + w.g1_seen);
+  a.bar = reinterpret_cast<int32_t *>(ws + w.bar);
+  a.status = reinterpret_cast<uint32_t *>(ws + w.status);
+  return a;
+}
+
+// [x permute] -> [plan] -> G1 -> G2 -> combine, or the fused layer kernel
+// (one launch).  The streaming and fused GEMMs stage x themselves; the
+// general and wide ones need its K-slot permuted copy in the workspace
+// (x_permuted: already written by the router).  With logits (fused only),
+// the fused kernel routes the tokens itself and writes ids / weights to
+// ids_out / topk_weights (workspace).
+int moe_forward_impl(const void *x, bool x_permuted, int64_t T, int H, int I, int E, int k,
+                     const int8_t *q1, const float *s1, const int8_t *q2, const float *s2, int bits,
+                     int64_t group_w1, int64_t group_w2, int flags, const int32_t *topk_ids,
+                     const float *topk_weights, char *ws, void *out, hipStream_t st, ProfileMarks &pm,
+                     int first_mark, const void *logits = nullptr, int ldt = LQ_F32, int renorm = 0,
+                     int32_t *ids_out = nullptr) {
+  const WsLayout w = ws_layout(T, H, I, E, k);
+  const int64_t g1 = effective_group(H, group_w1);
+  const int64_t g2 = effective_group(I, group_w2);
+  // the folded form applies one scale per 128-wide K chunk
+  const bool folded = (flags & LQ_MOE_FOLDED_SCALES) && g1 % kKC == 0 && g2 % kKC == 0;
+  const Path path = choose_path(bits, T, H, I, E, k, group_w1, group_w2, flags);
+  const bool stream = path == Path::kStream;
+  const bool fused = fused_eligible(path, folded, T, E, k, flags);
+
+  PlanArgs p = plan_args(topk_ids, T, E, k, ws, w);
+  if (path == Path::kWide) p.block_rows = kWRows;
+  MoeArgs a = layer_args(x, T, H, I, E, k, q1, s1, q2, s2, g1, g2, topk_ids, topk_weights, ws, w, p, out);
+  if (fused) {
+    if (logits) {
+      a.logits = logits;
+      a.ldt = ldt;
+      a.renorm = renorm;
+      a.ids_out = ids_out;
+      a.w_out = const_cast<float *>(topk_weights);
+    }
+    pm.mark(first_mark);
+    const int rc = bits == 4 ? launch_fused<4>(a, st) : launch_fused<8>(a, st);
+    if (rc) return rc;
+    for (int i = 1; i <= 3; ++i) pm.mark(first_mark + i);  // one launch: the later stages take no time
+    return pm.rc;
+  }
+  if (logits) return fail(LQ_ERR_RUNTIME, "moe_forward: in-kernel routing needs the fused layer kernel");
+  if (!stream && !x_permuted) {
+    const int64_t n8 = T * H / 8;
+    permute_rows_kernel<<<static_cast<int>(ceil_div(n8, 256)), 256, 0, st>>>(
+        static_cast<const uint16_t *>(x), n8, reinterpret_cast<uint16_t *>(ws + w.xperm));
+  }
+  // small layers on the streaming GEMMs plan their blocks in-kernel
+  // (every block of the in-kernel plan needs a CU of its own: there are at
+  // most ceil(T*k / 32) + min(E, T*k) blocks)
+  const int64_t nb_max = ceil_div(T * k, kRowsMax) + std::min<int64_t>(E, T * k);
+  const bool inplan =
+      stream && T * k <= kPlanMaxN && nb_max <= device_info().cus && device_info().cus <= kMaxSlots;
+  int rc = LQ_OK;
+  const int64_t nseg = ceil_div(T * k, kPlanSeg);
+  if (inplan) {
+    // no plan launch
+  } else if (nseg > 1) {  // large layers: one workgroup per segment of assignments
+    int32_t *segcnt = reinterpret_cast<int32_t *>(ws + w.segcnt);
+    plan_count_kernel<<<static_cast<int>(nseg), kPlanBlock, 0, st>>>(p, segcnt);
+    rc = check_launch("moe_plan_count");
+    if (rc) return rc;
+    plan_scatter_kernel<<<static_cast<int>(nseg), kPlanBlock, 0, st>>>(p, segcnt, static_cast<int>(nseg));
+    rc = check_launch("moe_plan_scatter");
+  } else {
+    plan_kernel<<<1, kPlanBlock, 0, st>>>(p);
+    rc = check_launch("moe_plan");
+  }
+  if (rc) return rc;
+  pm.mark(first_mark);
   const int64_t blocks = max_blocks_for(T, E, k);
   const int64_t max_g1 = blocks * (I / kF1), max_g2 = blocks * (H / kR2);
   if (bits == 4)
@@ -2370,6 +2880,26 @@ extern "C" size_t lq_moe_workspace_bytes(int64_t T, int H, int I, int E, int k) 
   return ws_layout(T, H, I, E, k).total;
 }
 
+extern "C" size_t lq_moe_sync_bytes(void) { return ws_layout(1, 1, 1, 1, 1).sync_end; }
+
+extern "C" int lq_moe_workspace_init(void *workspace, lq_stream_t stream) {
+  if (!workspace) return fail(LQ_ERR_VALUE, "moe_workspace_init: null workspace");
+  LQ_HIP_CHECK(hipMemsetAsync(workspace, 0, lq_moe_sync_bytes(), as_stream(stream)));
+  return LQ_OK;
+}
+
+extern "C" int lq_moe_status(const void *workspace, uint32_t *status, int clear, lq_stream_t stream) {
+  if (!workspace || !status) return fail(LQ_ERR_VALUE, "moe_status: null pointer");
+  const hipStream_t st = as_stream(stream);
+  LQ_HIP_CHECK(hipMemcpyAsync(status, workspace, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+  LQ_HIP_CHECK(hipStreamSynchronize(st));
+  if (clear && *status) {
+    // the counters of a call whose wait gave up may be left non-zero: clear the whole sync region
+    LQ_HIP_CHECK(hipMemsetAsync(const_cast<void *>(workspace), 0, lq_moe_sync_bytes(), st));
+  }
+  return LQ_OK;
+}
+
 extern "C" int lq_moe_profile_events(void *const *events, int n_events) {
   if (n_events < 0) return fail(LQ_ERR_VALUE, "moe_profile_events: negative count");
   t_prof_events = n_events ? events : nullptr;
@@ -2408,11 +2938,20 @@ extern "C" int lq_moe_layer(const void *x, const void *logits, int logits_dtype,
   int32_t *ids = topk_ids_out ? topk_ids_out : reinterpret_cast<int32_t *>(ws + w.ids);
   float *weights = reinterpret_cast<float *>(ws + w.weights);
   pm.mark(0);
-  const bool streaming = choose_path(bits, T, H, I, E, k, group_w1, group_w2, flags) == Path::kStream;
+  const Path path = choose_path(bits, T, H, I, E, k, group_w1, group_w2, flags);
+  const bool folded = (flags & LQ_MOE_FOLDED_SCALES) && effective_group(H, group_w1) % kKC == 0 &&
+                      effective_group(I, group_w2) % kKC == 0;
+  if (fused_eligible(path, folded, T, E, k, flags) && route_in_kernel(T, E)) {
+    if (logits_dtype != LQ_F32 && logits_dtype != LQ_BF16 && logits_dtype != LQ_F16)
+      return fail(LQ_ERR_VALUE, "route_topk: logits must be float32, float16 or bfloat16");
+    pm.mark(1);  // no router launch: the fused kernel routes
+    return moe_forward_impl(x, true, T, H, I, E, k, q1, s1, q2, s2, bits, group_w1, group_w2, flags, ids, weights,
+                            ws, out, st, pm, 2, logits, logits_dtype, renormalize, ids);
+  }
   // the general GEMMs stage the K-slot permuted copy of x the router writes
   rc = launch_route_topk(logits, logits_dtype, T, E, k, renormalize, ids, weights, st,
                          static_cast<const uint16_t *>(x), H,
-                         streaming ? nullptr : reinterpret_cast<uint16_t *>(ws + w.xperm));
+                         path == Path::kStream ? nullptr : reinterpret_cast<uint16_t *>(ws + w.xperm));
   if (rc) return rc;
   pm.mark(1);
   return moe_forward_impl(x, true, T, H, I, E, k, q1, s1, q2, s2, bits, group_w1, group_w2, flags, ids,

@@ -7,30 +7,69 @@ namespace lq {
 
 constexpr int kMaxExperts = 256;
 
-// Route token t with one wavefront: fp32 softmax over its E logits, top-k by
-// rank counting.  Lane l holds experts l, l+64, ... (EPL of them); each
-// expert's rank is rank(e) = #{e' : x[e'] > x[e], or x[e'] == x[e] and
-// e' < e} over the token's logits (broadcast lane by lane), so
-// ids come out in descending-logit order with ties to the lower expert id --
-// the order of descending probability, softmax being monotone -- with no
-// serial selection rounds.  Experts of rank < k write their id and fp32
-// softmax probability (renormalized over the k when renorm) to slot `rank`
-// of ids / weights, and the id also to ids_lds when it is not null.
-// Restates softmax(logits, -1, dtype=float32).topk(k) of
-// trajectory/llada.py:228-234.
-template <int LDT, int EPL>
-__device__ __forceinline__ void route_token(const void *__restrict__ logits, int64_t t, int E, int k, int renorm,
-                                            int32_t *__restrict__ ids, float *__restrict__ weights,
-                                            int32_t *ids_lds) {
+// Route one token with one wavefront from its logits v (lane l holds experts
+// l, l+64, ...: EPL of them; lanes past E hold -inf): fp32 softmax over the
+// E logits, top-k by rank counting.  Each expert's rank is rank(e) =
+// #{e' : x[e'] > x[e], or x[e'] == x[e] and e' < e} over the token's logits
+// (broadcast lane by lane), so ids come out in descending-logit order with
+// ties to the lower expert id -- the order of descending probability,
+// softmax being monotone -- with no serial selection rounds.  Experts of
+// rank < k call put(rank, e, p) with their fp32 softmax probability p
+// (renormalized over the k when renorm).  Restates
+// softmax(logits, -1, dtype=float32).topk(k) of trajectory/llada.py:228-234.
+// Routing of one token over E <= 64 experts (lane e = expert e; lanes past E
+// hold -inf), the cheap way.  softmax as route_values below.  The top-k set is found by a radix select on orderable
+// 32-bit keys of the logits (-0.0 taken as +0.0, so equal logits have equal
+// keys; lanes past E key 0, below every logit): 32 ballots of key >= c
+// build the k-th largest key from the top bit down; the set is every key
+// above it plus the lowest-numbered lanes equal to it.  Each selected lane's
+// rank is then counted against the k selected ones only: (greater key) or
+// (equal key and lower expert id).  The ids, their order and the weights
+// are those of the rank count in route_values.
+template <class Put>
+__device__ __forceinline__ void route_values64(float v, int E, int k, int renorm, Put put) {
   const int lane = threadIdx.x & 63;
-  float v[EPL];
+  const float m = wave_max(v);
+  const float p = lane < E ? expf(v - m) : 0.0f;
+  const float s = wave_sum(p);
+  const uint32_t u = __builtin_bit_cast(uint32_t, v == 0.0f ? 0.0f : v);
+  const uint32_t key = lane < E ? ((u & 0x80000000u) ? ~u : (u | 0x80000000u)) : 0u;
+  uint32_t thr = 0;
+#pragma unroll
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t c = thr | (1u << b);
+    thr = __popcll(__ballot(key >= c)) >= k ? c : thr;
+  }
+  const uint64_t gt = __ballot(key > thr);
+  uint64_t eq = __ballot(key == thr);
+  uint64_t sel = gt;
+  for (int need = k - __popcll(gt); need > 0; --need) {
+    const uint64_t low = eq & (~eq + 1);
+    sel |= low;
+    eq ^= low;
+  }
+  int rank = 0;
+  for (uint64_t rem = sel; rem; rem &= rem - 1) {
+    const int c = __builtin_ctzll(rem);
+    const uint32_t kc = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key), c));
+    rank += static_cast<int>(kc > key) + (static_cast<int>(kc == key) & static_cast<int>(c < lane));
+  }
+  const bool mine = (sel >> lane) & 1;
+  const float pw = p / s;
+  const float wsum = renorm ? wave_sum(mine ? pw : 0.0f) : 1.0f;
+  if (mine) put(rank, lane, renorm ? pw / wsum : pw);
+}
+
+template <int EPL, class Put>
+__device__ __forceinline__ void route_values(const float (&v)[EPL], int E, int k, int renorm, Put put) {
+  if constexpr (EPL == 1) {
+    route_values64(v[0], E, k, renorm, put);
+    return;
+  }
+  const int lane = threadIdx.x & 63;
   float m = -__builtin_inff();
 #pragma unroll
-  for (int j = 0; j < EPL; ++j) {
-    const int e = lane + 64 * j;
-    v[j] = e < E ? load_f32<LDT>(logits, t * E + e) : -__builtin_inff();
-    m = fmaxf(m, v[j]);
-  }
+  for (int j = 0; j < EPL; ++j) m = fmaxf(m, v[j]);
   m = wave_max(m);
   float p[EPL];
   float s = 0.0f;
@@ -44,19 +83,21 @@ __device__ __forceinline__ void route_token(const void *__restrict__ logits, int
   int rank[EPL];
 #pragma unroll
   for (int j = 0; j < EPL; ++j) rank[j] = 0;
-  // every logit is broadcast from its lane (v_readlane: no LDS round trip)
+  // every logit is broadcast from its lane (v_readlane: no LDS round trip).
+  // No test of c < E: a lane past E holds -inf, which is greater than no
+  // logit, and equal ones count only for a lower index, which c >= E is
+  // not for any e < E.  The terms are combined without short-circuiting so
+  // the loop stays straight-line.
 #pragma unroll
   for (int jc = 0; jc < EPL; ++jc) {
 #pragma unroll
     for (int l = 0; l < 64; ++l) {
       const int c = 64 * jc + l;
-      if (c < E) {
-        const float xc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[jc]), l));
+      const float xc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[jc]), l));
 #pragma unroll
-        for (int j = 0; j < EPL; ++j) {
-          const int e = lane + 64 * j;
-          rank[j] += (xc > v[j] || (xc == v[j] && c < e)) ? 1 : 0;
-        }
+      for (int j = 0; j < EPL; ++j) {
+        const int e = lane + 64 * j;
+        rank[j] += static_cast<int>(xc > v[j]) + (static_cast<int>(xc == v[j]) & static_cast<int>(c < e));
       }
     }
   }
@@ -72,11 +113,30 @@ __device__ __forceinline__ void route_token(const void *__restrict__ logits, int
     const int e = lane + 64 * j;
     if (e < E && rank[j] < k) {
       const float pw = p[j] / s;
-      ids[t * k + rank[j]] = e;
-      weights[t * k + rank[j]] = renorm ? pw / wsum : pw;
-      if (ids_lds) ids_lds[t * k + rank[j]] = e;
+      put(rank[j], e, renorm ? pw / wsum : pw);
     }
   }
+}
+
+// Route token t of logits [T, E] (dtype LDT) with one wavefront: writes its k
+// ids and weights to slots t*k .. t*k + k-1 of ids / weights, and the ids also
+// to ids_lds when it is not null (route_values).
+template <int LDT, int EPL>
+__device__ __forceinline__ void route_token(const void *__restrict__ logits, int64_t t, int E, int k, int renorm,
+                                            int32_t *__restrict__ ids, float *__restrict__ weights,
+                                            int32_t *ids_lds) {
+  const int lane = threadIdx.x & 63;
+  float v[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int e = lane + 64 * j;
+    v[j] = e < E ? load_f32<LDT>(logits, t * E + e) : -__builtin_inff();
+  }
+  route_values<EPL>(v, E, k, renorm, [&](int rank, int e, float w) __attribute__((always_inline)) {
+    ids[t * k + rank] = e;
+    weights[t * k + rank] = w;
+    if (ids_lds) ids_lds[t * k + rank] = e;
+  });
 }
 
 // Stable expert permutation (the plan kernel of lq_moe.hip without its work

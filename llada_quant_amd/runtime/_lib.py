@@ -22,11 +22,12 @@ LIB_PATH = os.path.join(_PKG_DIR, "liblladaq.so")
 LQ_OK, LQ_ERR_VALUE, LQ_ERR_UNSUPPORTED, LQ_ERR_RUNTIME = 0, 1, 2, 3
 LQ_F32, LQ_F16, LQ_BF16 = 0, 1, 2
 LQ_SCALE_AMAX, LQ_SCALE_MSE = 0, 1
-ABI_VERSION = 2
+ABI_VERSION = 3
 LQ_MOE_FOLDED_SCALES = 1
 LQ_MOE_GENERAL_KERNEL = 2
 LQ_MOE_WIDE_KERNEL = 4
 LQ_MOE_STREAM_KERNEL = 8
+LQ_MOE_FUSED_LAYER = 16
 
 DTYPE_CODES = {torch.float32: LQ_F32, torch.float16: LQ_F16, torch.bfloat16: LQ_BF16}
 
@@ -50,6 +51,9 @@ SIGNATURES = {
     "lq_moe_layer": (_I32, [_P, _P, _I32, _I64, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _I32, _I64, _I64,
                             _I32, _P, _SZ, _P, _P, _P]),
     "lq_moe_profile_events": (_I32, [_P, _I32]),
+    "lq_moe_sync_bytes": (_SZ, []),
+    "lq_moe_workspace_init": (_I32, [_P, _P]),
+    "lq_moe_status": (_I32, [_P, _P, _I32, _P]),
     "lq_quant_linear": (_I32, [_P, _I64, _I32, _I32, _P, _P, _I32, _I64, _I32, _P, _SZ, _P, _P]),
     "lq_linear_workspace_bytes": (_SZ, [_I64, _I32, _I32]),
     "lq_route_gemm_topk": (_I32, [_P, _P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P]),
@@ -129,3 +133,26 @@ def dtype_code(dtype: torch.dtype, what: str) -> int:
         return DTYPE_CODES[dtype]
     except KeyError:
         raise ValueError(f"{what} must be float32, float16 or bfloat16, got {dtype}") from None
+
+
+def moe_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """A MoE workspace of at least ``nbytes`` bytes whose sync region is zero.
+
+    The library's MoE calls need the sync region at the start of their
+    workspace zero on entry and leave it zero, so a workspace allocated here
+    serves any number of later calls (one stream at a time).
+    """
+    n = max(int(nbytes), int(load().lq_moe_sync_bytes()), 1)
+    return torch.zeros(n, dtype=torch.uint8, device=device)
+
+
+def check_status(workspace: torch.Tensor, what: str) -> None:
+    """With ``LLADAQ_CHECK_STATUS=1``: synchronise and raise if a bounded wait of the
+    kernels gave up since the last check (their output is then wrong)."""
+    if os.environ.get("LLADAQ_CHECK_STATUS", "0") in ("", "0"):
+        return
+    st = ctypes.c_uint32(0)
+    rc = load().lq_moe_status(ptr(workspace), ctypes.byref(st), 1, stream(workspace.device))
+    check(rc, what)
+    if st.value:
+        raise RuntimeError(f"{what}: a kernel's bounded wait gave up (status 0x{st.value:x}); the output is wrong")

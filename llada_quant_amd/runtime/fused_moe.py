@@ -46,6 +46,12 @@ def workspace_bytes(tokens: int, hidden: int, intermediate: int, num_experts: in
     return int(_lib.load().lq_moe_workspace_bytes(tokens, hidden, intermediate, num_experts, top_k))
 
 
+def moe_workspace(tokens: int, hidden: int, intermediate: int, num_experts: int, top_k: int,
+                  device: torch.device) -> torch.Tensor:
+    """A zero-initialised workspace for layers of this shape (reusable across calls on one stream)."""
+    return _lib.moe_workspace(workspace_bytes(tokens, hidden, intermediate, num_experts, top_k), device)
+
+
 def fused_moe_packed(
     x: torch.Tensor,
     w1: QuantResult,
@@ -58,6 +64,7 @@ def fused_moe_packed(
     general_kernel: bool = False,
     wide_kernel: bool = False,
     stream_kernel: bool = False,
+    fused_layer: bool = False,
 ) -> torch.Tensor:
     """The layer on explicit operands: ``x [T, H]`` bf16, int32 ids and fp32 weights ``[T, k]``.
 
@@ -70,7 +77,12 @@ def fused_moe_packed(
     ones apply, ``wide_kernel`` the wide (matrix-core) ones, which layers with
     at least 32 routed rows per expert on average take by themselves, and
     ``stream_kernel`` the streaming (weight-bandwidth) ones, which smaller
-    layers take (same results bit for bit; for comparison).
+    layers take (same results bit for bit; for comparison).  ``fused_layer``
+    runs a small streaming-family layer (E <= 64, T*k <= 2048) as one launch,
+    the fused layer kernel, instead of GEMM1, GEMM2 and combine (same bits).  A ``workspace``
+    passed in must come from :func:`moe_workspace` (or otherwise start with a
+    zero sync region, ``lq_moe_sync_bytes`` bytes); it may be reused by later
+    calls on the same stream.
     """
     g1, g2, I = _check_weights(x, w1, w2)
     T, H = x.shape
@@ -89,11 +101,12 @@ def fused_moe_packed(
     tc = max(c1 - c0 for c0, c1 in spans)
     ws_need = workspace_bytes(tc, H, I, E, k)
     if workspace is None or workspace.numel() < ws_need:
-        workspace = torch.empty(max(ws_need, 1), dtype=torch.uint8, device=device)
+        workspace = _lib.moe_workspace(ws_need, device)
     flags = (_moe_flags(folded_scales)
              | (_lib.LQ_MOE_GENERAL_KERNEL if general_kernel else 0)
              | (_lib.LQ_MOE_WIDE_KERNEL if wide_kernel else 0)
-             | (_lib.LQ_MOE_STREAM_KERNEL if stream_kernel else 0))
+             | (_lib.LQ_MOE_STREAM_KERNEL if stream_kernel else 0)
+             | (_lib.LQ_MOE_FUSED_LAYER if fused_layer else 0))
     if T:
         lib = _lib.load()
         with torch.cuda.device(device):
@@ -104,6 +117,7 @@ def fused_moe_packed(
                     workspace.numel(), _lib.ptr(out[c0:c1]), _lib.stream(device),
                 )
                 _lib.check(rc, "fused_moe")
+        _lib.check_status(workspace, "fused_moe")
     return out
 
 
@@ -213,12 +227,15 @@ def moe_layer(
     top_k: int,
     renormalize: bool = False,
     folded_scales: bool = False,
+    fused_layer: bool = False,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """Router + quantized experts in one library call: ``(output [..., H], topk_ids [T, k] int32)``.
 
     ``router_logits [..., E]`` are the gate's outputs; routing is
     softmax(fp32) -> top-k (descending probability, ties to the lower id),
     weights renormalized over the k experts when ``renormalize``.
+    ``fused_layer``: a small streaming-family layer runs as one launch, which
+    also routes when T <= 64 (same results).
     """
     q1 = _unpack_weight(w1, "w1")
     q2 = _unpack_weight(w2, "w2")
@@ -243,7 +260,7 @@ def moe_layer(
     ids = torch.empty(T, top_k, dtype=torch.int32, device=device)
     spans = _chunks(T, max_tokens_per_call(H, I, top_k))
     tc = max(c1 - c0 for c0, c1 in spans)
-    workspace = torch.empty(max(workspace_bytes(tc, H, I, E, top_k), 1), dtype=torch.uint8, device=device)
+    workspace = _lib.moe_workspace(workspace_bytes(tc, H, I, E, top_k), device)
     if T:
         lib = _lib.load()
         code = _lib.dtype_code(logits.dtype, "router_logits")
@@ -252,8 +269,10 @@ def moe_layer(
                 rc = lib.lq_moe_layer(
                     _lib.ptr(xc[c0:c1]), _lib.ptr(logits[c0:c1]), code, c1 - c0, H, I, E, top_k, int(renormalize),
                     _lib.ptr(q1c), _lib.ptr(s1), _lib.ptr(q2c), _lib.ptr(s2), q1.bits, g1, g2,
-                    _moe_flags(folded_scales), _lib.ptr(workspace), workspace.numel(), _lib.ptr(out[c0:c1]),
+                    _moe_flags(folded_scales) | (_lib.LQ_MOE_FUSED_LAYER if fused_layer else 0),
+                    _lib.ptr(workspace), workspace.numel(), _lib.ptr(out[c0:c1]),
                     _lib.ptr(ids[c0:c1]), _lib.stream(device),
                 )
                 _lib.check(rc, "moe_layer")
+        _lib.check_status(workspace, "moe_layer")
     return out.reshape(hidden_states.shape), ids

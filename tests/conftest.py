@@ -22,6 +22,11 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
+# every MoE call in the tests reads back its workspace's status word: a
+# bounded wait inside a kernel that gave up fails the test instead of passing
+# wrong numbers silently
+os.environ.setdefault("LLADAQ_CHECK_STATUS", "1")
+
 HIDDEN = 128
 INTERMEDIATE = 64
 NUM_EXPERTS = 4

@@ -19,7 +19,7 @@ import torch
 
 from conftest import bits_u16
 from llada_quant_amd.algorithms.symmetric import quantize_tensor
-from llada_quant_amd.runtime.fused_moe import fused_moe, fused_moe_packed, moe_layer, workspace_bytes
+from llada_quant_amd.runtime.fused_moe import fused_moe, fused_moe_packed, moe_layer, moe_workspace
 from llada_quant_amd.runtime.routing import route_topk
 from oracle import oracle as O
 from test_gpu_route import zipf_logits
@@ -44,9 +44,14 @@ def oracle_out(x, q1, q2, ids, weights, rows=None):
     xs = x if rows is None else x[rows]
     ids_np = ids.cpu().numpy() if rows is None else ids.cpu().numpy()[rows]
     w_np = weights.cpu().numpy() if rows is None else weights.cpu().numpy()[rows]
-    d1 = bits_u16(q1.dequantize(torch.bfloat16))
-    d2 = bits_u16(q2.dequantize(torch.bfloat16))
+    d1 = oracle_dequant(q1)
+    d2 = oracle_dequant(q2)
     return O.moe_forward(bits_u16(xs), d1, d2, ids_np, w_np)
+
+
+def oracle_dequant(q) -> np.ndarray:
+    """bf16 bits of the reference's dequantized weight, from the CPU oracle (not the HIP kernel)."""
+    return O.dequant(q.q.cpu().numpy(), q.scale.cpu().numpy(), q.bits, q.group_size, q.logical_shape[-1])
 
 
 def assert_close(out: torch.Tensor, ref: np.ndarray, mean_rel_bar: float = MEAN_REL):
@@ -116,19 +121,19 @@ def test_c4_zipf_skew_full(dev, folded):
     ids, w = route_topk(zipf_logits(64, 64, seed=4).to(dev), 8)
     counts = torch.bincount(ids.reshape(-1).long().cpu(), minlength=64)
     assert (counts == 0).any() and counts.max() > 16  # the skew really is there
-    ws = torch.empty(workspace_bytes(64, 2048, 1024, 64, 8), dtype=torch.uint8, device=dev)
+    ws = moe_workspace(64, 2048, 1024, 64, 8, dev)
     out = fused_moe_packed(x, q1, q2, ids, w, workspace=ws, folded_scales=folded)
     assert_close(out, oracle_out(x, q1, q2, ids, w), bar(folded))
 
 
 @pytest.mark.parametrize("folded", [False, True])
 def test_c3_large_token_count_sampled(dev, folded):
-    """C3: INT4, 4096 tokens, top-8 (~512 rows per expert), oracle on 48 sampled tokens."""
-    q1, q2 = make_layer(dev, 64, 2048, 1024, 4, seed=3)
+    """C3: INT4 MSE (grid 16), 4096 tokens, top-8 (~512 rows per expert), oracle on 48 sampled tokens."""
+    q1, q2 = make_layer(dev, 64, 2048, 1024, 4, seed=3, search="mse", grid=16)
     g = torch.Generator().manual_seed(3)
     x = torch.randn(4096, 2048, generator=g).to(torch.bfloat16).to(dev)
     ids, w = route_topk(torch.randn(4096, 64, generator=g).to(dev), 8)
-    ws = torch.empty(workspace_bytes(4096, 2048, 1024, 64, 8), dtype=torch.uint8, device=dev)
+    ws = moe_workspace(4096, 2048, 1024, 64, 8, dev)
     out = fused_moe_packed(x, q1, q2, ids, w, workspace=ws, folded_scales=folded)
     rows = np.sort(np.random.default_rng(3).choice(4096, 48, replace=False))
     assert_close(out[torch.from_numpy(rows).to(dev)], oracle_out(x, q1, q2, ids, w, rows), bar(folded))
@@ -353,3 +358,76 @@ def test_moe_layer_front_end_matches_router_then_forward(dev, T, k, E, renorm):
     ref = fused_moe_packed(x, q1, q2, ids2, w2)
     assert torch.equal(out, ref)
     assert_close(out, oracle_out(x, q1, q2, ids2, w2))
+
+
+@pytest.mark.parametrize("E,H,I,T,k,bits,skew", [
+    (64, 2048, 1024, 64, 8, 4, True),    # C4: Zipf skew, empty and hot experts, two-block experts
+    (64, 2048, 1024, 33, 8, 8, False),   # INT8, ragged T
+    (16, 1024, 512, 7, 2, 4, True),      # few rows: most CUs share a few blocks
+    (8, 512, 512, 200, 1, 4, False),     # top-1, several blocks per expert
+    (64, 1024, 1024, 256, 8, 4, False),  # the most assignments one workgroup plans (2048)
+])
+def test_fused_layer_matches_general_kernels(dev, E, H, I, T, k, bits, skew):
+    """The fused layer kernel (plan, GEMM1, GEMM2 and combine in one launch, the
+    workgroups handing gate/up rows and slot outputs to each other) does the
+    general kernels' per-chunk arithmetic in the same order: the same bits."""
+    q1, q2 = make_layer(dev, E, H, I, bits, seed=T + E + bits, search="mse" if bits == 4 else "amax")
+    g = torch.Generator().manual_seed(T + 3)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    logits = zipf_logits(T, E, seed=T) if skew else torch.randn(T, E, generator=g)
+    ids, w = route_topk(logits.to(dev), k)
+    a = fused_moe_packed(x, q1, q2, ids, w, fused_layer=True)
+    b = fused_moe_packed(x, q1, q2, ids, w, general_kernel=True)
+    assert torch.equal(a, b)
+    assert_close(a, oracle_out(x, q1, q2, ids, w))
+
+
+def test_fused_layer_invalid_ids_and_empty_layer(dev):
+    """ids outside [0, E) contribute nothing in the fused kernel too; a layer whose ids
+    are all invalid writes zeros."""
+    E, H, I, T, k = 16, 1024, 512, 40, 3
+    q1, q2 = make_layer(dev, E, H, I, 4, seed=9)
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    ids = torch.randint(0, E, (T, k), generator=g, dtype=torch.int32)
+    ids[::5, 1] = -1
+    ids[::7, 2] = E
+    ids[3] = -1  # a token with no valid slot
+    w = torch.rand(T, k, generator=g)
+    a = fused_moe_packed(x, q1, q2, ids.to(dev), w.to(dev), fused_layer=True)
+    assert torch.equal(a, fused_moe_packed(x, q1, q2, ids.to(dev), w.to(dev), general_kernel=True))
+    assert not a[3].any()
+    none = torch.full((T, k), -1, dtype=torch.int32, device=dev)
+    assert not fused_moe_packed(x, q1, q2, none, w.to(dev), fused_layer=True).any()
+
+
+@pytest.mark.parametrize("T,renorm", [(64, False), (5, True), (64, True)])
+def test_fused_layer_routes_in_kernel(dev, T, renorm):
+    """moe_layer with the fused kernel at T <= 64: workgroup t routes token t with the router
+    kernel's arithmetic; ids and output equal route_topk + fused_moe_packed bit for bit."""
+    E, H, I, k = 64, 2048, 1024, 8
+    q1, q2 = make_layer(dev, E, H, I, 4, seed=T, search="mse")
+    g = torch.Generator().manual_seed(T + 11)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    logits = zipf_logits(T, E, seed=T + 1).to(dev)
+    out, ids = moe_layer(x, logits, q1, q2, top_k=k, renormalize=renorm, fused_layer=True)
+    ids2, w2 = route_topk(logits, k, renormalize=renorm)
+    assert torch.equal(ids, ids2)
+    assert torch.equal(out, fused_moe_packed(x, q1, q2, ids2, w2))
+    assert_close(out, oracle_out(x, q1, q2, ids2, w2))
+
+
+def test_fused_layer_back_to_back_calls_reuse_the_workspace(dev):
+    """Every fused call leaves the workspace's sync counters at zero: ten calls in a row on one
+    workspace, with different routing and token counts, each equal to the separate launches
+    (the status word is read back after every call: no wait gave up)."""
+    E, H, I, k = 64, 2048, 1024, 8
+    q1, q2 = make_layer(dev, E, H, I, 4, seed=77, search="mse")
+    ws = moe_workspace(64, H, I, E, k, dev)
+    for i in range(10):
+        T = [64, 17, 64, 1, 40][i % 5]
+        g = torch.Generator().manual_seed(100 + i)
+        x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+        ids, w = route_topk(zipf_logits(T, E, seed=200 + i).to(dev), k)
+        a = fused_moe_packed(x, q1, q2, ids, w, workspace=ws, fused_layer=True)
+        assert torch.equal(a, fused_moe_packed(x, q1, q2, ids, w)), f"call {i}"
