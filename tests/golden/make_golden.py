@@ -10,7 +10,8 @@ stores inputs and outputs as ``.npz`` fixtures next to it.
 Run in the build container only (the reference tree does not exist on the
 GPU box):
 
-    python tests/golden/make_golden.py [/root/reference]
+    python tests/golden/make_golden.py [/root/reference]          # all but the w1 hash
+    python tests/golden/make_golden.py /root/reference c5w1       # the C5 w1 hash
 
 The fixtures are data: inputs as bit patterns, outputs as the reference
 returned them.  Nothing here is shipped or imported by the product.
@@ -54,9 +55,35 @@ def _cases():
     yield "f16_g128_int4_grid16", f16, 4, 128, 16
 
 
-def main(reference_root: str) -> None:
+def c5_hash_fixture(quantize_tensor, name: str, shape, seed: int) -> None:
+    """A C5-sized tensor (bf16 ~N(0, 0.02), INT4, G=128, MSE grid 16): too big to store, so
+    store the seed and the SHA-256 of the reference's q and scale bytes."""
+    gen = torch.Generator().manual_seed(seed)
+    w = (torch.randn(*shape, generator=gen) * 0.02).to(torch.bfloat16)
+    res = quantize_tensor(w, bits=4, group_size=128, scale_search="mse", search_grid=16)
+    np.savez_compressed(
+        os.path.join(HERE, f"mse_c5_{name}_layer_hash.npz"),
+        seed=np.int64(seed),
+        shape=np.array(w.shape, np.int64),
+        std=np.float64(0.02),
+        bits=np.int32(4),
+        group_size=np.int32(128),
+        grid=np.int32(16),
+        q_sha256=np.frombuffer(hashlib.sha256(res.q.numpy().tobytes()).digest(), np.uint8),
+        scale_sha256=np.frombuffer(hashlib.sha256(res.scale.numpy().tobytes()).digest(), np.uint8),
+        scale_head=res.scale.reshape(-1)[:4096].numpy(),
+    )
+    print("wrote c5", name, "hash fixture")
+
+
+def main(reference_root: str, only: str = "") -> None:
     sys.path.insert(0, os.path.join(reference_root, "src"))
     from LLaDA_Quant.algorithms.symmetric import quantize_tensor  # noqa: E402
+
+    if only == "c5w1":
+        # a full w1 of one C5 layer: [64, 2 * 1024, 2048] (gate and up rows)
+        c5_hash_fixture(quantize_tensor, "w1", (64, 2048, 2048), 20251202)
+        return
 
     torch.manual_seed(0)
     for name, w, bits, group, grid in _cases():
@@ -77,26 +104,10 @@ def main(reference_root: str) -> None:
         )
         print("wrote", name, tuple(w.shape), "q", tuple(res.q.shape), "scale", tuple(res.scale.shape))
 
-    # one C5-sized tensor (a full w2 of one layer: [64, 2048, 1024] bf16,
-    # ~N(0, 0.02), INT4, G=128, grid 16): too big to store, so store the
-    # seed and SHA-256 of the reference's q and scale bytes.
-    gen = torch.Generator().manual_seed(20251201)
-    w2 = (torch.randn(64, 2048, 1024, generator=gen) * 0.02).to(torch.bfloat16)
-    res = quantize_tensor(w2, bits=4, group_size=128, scale_search="mse", search_grid=16)
-    np.savez_compressed(
-        os.path.join(HERE, "mse_c5_w2_layer_hash.npz"),
-        seed=np.int64(20251201),
-        shape=np.array(w2.shape, np.int64),
-        std=np.float64(0.02),
-        bits=np.int32(4),
-        group_size=np.int32(128),
-        grid=np.int32(16),
-        q_sha256=np.frombuffer(hashlib.sha256(res.q.numpy().tobytes()).digest(), np.uint8),
-        scale_sha256=np.frombuffer(hashlib.sha256(res.scale.numpy().tobytes()).digest(), np.uint8),
-        scale_head=res.scale.reshape(-1)[:4096].numpy(),
-    )
-    print("wrote c5 hash fixture")
+    # one C5-sized w2 of one layer: [64, 2048, 1024]
+    c5_hash_fixture(quantize_tensor, "w2", (64, 2048, 1024), 20251201)
+    # and a w1 ([64, 2048, 2048]): python tests/golden/make_golden.py <root> c5w1
 
 
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference", sys.argv[2] if len(sys.argv) > 2 else "")

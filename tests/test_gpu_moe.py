@@ -431,3 +431,27 @@ def test_fused_layer_back_to_back_calls_reuse_the_workspace(dev):
         ids, w = route_topk(zipf_logits(T, E, seed=200 + i).to(dev), k)
         a = fused_moe_packed(x, q1, q2, ids, w, workspace=ws, fused_layer=True)
         assert torch.equal(a, fused_moe_packed(x, q1, q2, ids, w)), f"call {i}"
+
+
+def test_c5_layer_full_size(dev):
+    """C5: one layer of the 16-layer stack at full size -- E=64, H=2048, I=1024, INT4 with MSE
+    grid-16 scales, 32 x 1024 = 32768 tokens, top-8.  moe_layer runs it as two library calls of
+    16384 tokens (one call addresses T*k*H*4 < 2^31 bytes).  The routing of all 32768 tokens is
+    bit-exact against torch's softmax(fp32).topk on the CPU, and 32 sampled token rows against
+    the oracle."""
+    from llada_quant_amd.runtime.fused_moe import _chunks, max_tokens_per_call
+
+    E, H, I, T, k = 64, 2048, 1024, 32768, 8
+    assert len(_chunks(T, max_tokens_per_call(H, I, k))) == 2
+    q1, q2 = make_layer(dev, E, H, I, 4, seed=55, search="mse", grid=16)
+    g = torch.Generator().manual_seed(55)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    logits = torch.randn(T, E, generator=g)
+    out, ids = moe_layer(x.to(dev), logits.to(dev), q1, q2, top_k=k)
+    ref_ids = torch.softmax(logits, dim=-1, dtype=torch.float32).topk(k, dim=-1).indices
+    assert torch.equal(ids.cpu().long(), ref_ids)
+    ids_o, w_o = O.route_topk(logits.numpy(), k, False)
+    assert np.array_equal(ids.cpu().numpy(), ids_o)
+    rows = np.sort(np.random.default_rng(55).choice(T, 32, replace=False))
+    ref = O.moe_forward(bits_u16(x[rows]), oracle_dequant(q1), oracle_dequant(q2), ids_o[rows], w_o[rows])
+    assert_close(out[torch.from_numpy(rows).to(dev)], ref)

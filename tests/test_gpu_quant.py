@@ -169,9 +169,11 @@ def test_quantize_matches_reference_golden_vectors(dev, path):
     assert np.array_equal(bits_u16(res.dequantize(torch.bfloat16)), z["dequant_bf16"])
 
 
-def test_quantize_c5_layer_matches_reference_hash(dev):
-    """A C5 w2 ([64, 2048, 1024] bf16, INT4 G=128, MSE grid 16) gives the reference's exact bytes."""
-    z = np.load(os.path.join(GOLDEN, "mse_c5_w2_layer_hash.npz"))
+@pytest.mark.parametrize("which", ["w2", "w1"])
+def test_quantize_c5_layer_matches_reference_hash(dev, which):
+    """A C5 w2 ([64, 2048, 1024]) and w1 ([64, 2048, 2048]), bf16 ~N(0, 0.02), INT4 G=128,
+    MSE grid 16: the GPU quantizer gives the reference quantizer's exact bytes."""
+    z = np.load(os.path.join(GOLDEN, f"mse_c5_{which}_layer_hash.npz"))
     gen = torch.Generator().manual_seed(int(z["seed"]))
     w = (torch.randn(*z["shape"].tolist(), generator=gen) * float(z["std"])).to(torch.bfloat16)
     res = quantize_tensor(w.to(dev), bits=4, group_size=128, scale_search="mse", search_grid=int(z["grid"]))

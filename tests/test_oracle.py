@@ -368,3 +368,55 @@ def test_torch_reference_layer_agrees_with_the_oracle():
     ref = O.moe_forward(bf16_bits(x), O.dequant(q1, s1, 4, 128, H), O.dequant(q2, s2, 4, 128, I), oids, ow)
     diff = np.abs(out.float().numpy() - ref)
     assert diff.max() < 2e-2 and diff.sum() / np.abs(ref).sum() < 5e-3
+
+
+# ---------------------------------------------------------------------------
+# the MoE forward against the reference's own executable restatements
+# ---------------------------------------------------------------------------
+
+def _moe_golden_cases():
+    import sys
+
+    sys.path.insert(0, GOLDEN)
+    import moe_inputs
+
+    return moe_inputs
+
+
+@pytest.mark.parametrize("case", [c[0] for c in _moe_golden_cases().CASES])
+def test_moe_forward_matches_reference_expert_forward(case):
+    """oq_moe_forward against the reference's expert_forward (benchmarks/bench_numerical.py:28-36)
+    and FusedExpertBlock.forward (tests/unit/conftest.py:37-43), both executed by
+    tests/golden/make_moe_golden.py on the reference-quantized weights.  Those are dense over
+    every expert and averaged, so the oracle runs with every token routed to all E experts at
+    weight 1/E.  They accumulate gate, up and act in fp32 where fused_moe rounds each to bf16,
+    so the match is to the north-star tolerance (max-abs 2e-2, mean-relative 5e-3), which a
+    swapped gate/up split, a missing SwiGLU factor or a transposed down projection all exceed.
+    The oracle's quantize + dequant must first reproduce the reference's dequantized bytes."""
+    mi = _moe_golden_cases()
+    name, E, H, I, T, bits, group, search, grid, seed = next(c for c in mi.CASES if c[0] == case)
+    z = np.load(os.path.join(GOLDEN, f"moe_{name}.npz"))
+    w1b, w2b, xb = mi.case_inputs(E, H, I, T, seed)
+    deq = []
+    for wb, k, key in ((w1b, H, "d1_sha256"), (w2b, I, "d2_sha256")):
+        q, s, g = O.quantize(wb, bits=bits, group_size=group, scale_search=search, grid=grid, w_dtype=O.BF16)
+        d = O.dequant(q, s, bits, g, k)
+        assert hashlib.sha256(d.astype(np.uint16).tobytes()).digest() == z[key].tobytes(), key
+        deq.append(d)
+    d1, d2 = deq
+    ids = np.tile(np.arange(E, dtype=np.int32), (T, 1))
+    wts = np.full((T, E), 1.0 / E, np.float32)
+    got = O.moe_forward(xb, d1, d2, ids, wts).astype(np.float64)
+
+    def close(ref):
+        diff = np.abs(got - ref)
+        return diff.max() < 2e-2 and diff.sum() / np.abs(ref).sum() < 5e-3
+
+    ref = z["expert_forward"].astype(np.float64)
+    assert close(ref), (np.abs(got - ref).max(), np.abs(got - ref).sum() / np.abs(ref).sum())
+    assert close(z["fused_block_forward"].astype(np.float64))
+    # planted slips the check must catch
+    swapped = np.concatenate([d1[:, I:], d1[:, :I]], axis=1)
+    assert not close(O.moe_forward(xb, swapped, d2, ids, wts).astype(np.float64))
+    d2t = np.ascontiguousarray(d2.reshape(E, H, I)[:, ::-1, :])  # rows of W2 in the wrong order
+    assert not close(O.moe_forward(xb, d1, d2t, ids, wts).astype(np.float64))
