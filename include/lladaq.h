@@ -255,6 +255,25 @@ int lq_moe_layer(const void *x, const void *logits, int logits_dtype,
                  lq_stream_t stream);
 
 /*
+ * lq_moe_layer without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops and
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * workspace is a 64 MiB device array inside the library (one per GPU, held
+ * until the process ends); a layer whose lq_moe_workspace_bytes exceeds it
+ * is rejected with LQ_ERR_UNSUPPORTED.  Allocates nothing: no hipMalloc or
+ * hipFree.  Each call first clears the array's sync region with a kernel.
+ * Every call on one GPU shares that array, so calls that overlap on one GPU
+ * (two streams, two threads) race and give wrong results; the bounded-wait
+ * status word is not reported.  Arguments and results as lq_moe_layer.
+ */
+int lq_moe_layer_noalloc(const void *x, const void *logits, int logits_dtype,
+                         int64_t T, int H, int I, int E, int k,
+                         int renormalize, const int8_t *q1, const float *s1,
+                         const int8_t *q2, const float *s2, int bits,
+                         int64_t group_w1, int64_t group_w2, int flags,
+                         void *out, int32_t *topk_ids_out, lq_stream_t stream);
+
+/*
  * Measurement hook (no counterpart in the reference; its timing is host-side,
  * benchmarks/bench_generation_latency.py:51-72).  Registers caller-owned
  * hipEvent_t handles that the NEXT lq_moe_forward / lq_moe_layer call on

@@ -2958,6 +2958,78 @@ extern "C" int lq_moe_layer(const void *x, const void *logits, int logits_dtype,
                           weights, ws, out, st, pm, 2);
 }
 
+// ---------------------------------------------------------------------------
+// allocation-free layer: the workspace is a file-scope device array
+// ---------------------------------------------------------------------------
+
+namespace lq {
+
+// Each GPU the library runs on holds its own copy of this array from the
+// code object's load to the end of the process.  64 MiB covers every layer
+// whose per-assignment buffers fit: T*k*H*4 (the fp32 partial outputs) is the
+// largest term, 32 MiB at T*k = 4096 with H = 2048.
+constexpr size_t kScratchBytes = size_t{64} << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+// Device addresses of `scratch`, one per device, taken once with that device
+// current.  The host-side name `scratch` is not a device address: only these
+// pointers reach kernels.
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+char *g_scratch_ptr[kScratchDevices] = {};
+
+int scratch_on_current_device(char **out) {
+  int dev = 0;
+  LQ_HIP_CHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kScratchDevices)
+    return fail(LQ_ERR_UNSUPPORTED, "moe_layer_noalloc: device index " + std::to_string(dev) + " out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    LQ_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return fail(LQ_ERR_RUNTIME, "moe_layer_noalloc: hipGetSymbolAddress gave a null address");
+    g_scratch_ptr[dev] = static_cast<char *>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return LQ_OK;
+}
+
+// Clears n 32-bit words with vector stores (a kernel rather than a memset
+// node, so a captured call replays it as well).
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t *__restrict__ p, int n) {
+  for (int i = threadIdx.x; i < n; i += 256) p[i] = 0u;
+}
+
+}  // namespace lq
+
+extern "C" int lq_moe_layer_noalloc(const void *x, const void *logits, int logits_dtype, int64_t T, int H, int I,
+                                    int E, int k, int renormalize, const int8_t *q1, const float *s1,
+                                    const int8_t *q2, const float *s2, int bits, int64_t group_w1,
+                                    int64_t group_w2, int flags, void *out, int32_t *topk_ids_out,
+                                    lq_stream_t stream) {
+  // shape errors other than the scratch limit are lq_moe_layer's to report
+  if (T >= 0 && T <= (int64_t{1} << 18) && H > 0 && I > 0 && E > 0 && E <= kMaxExperts && k > 0 && k <= E) {
+    const size_t need = ws_layout(T, H, I, E, k).total;
+    if (need > kScratchBytes)
+      return fail(LQ_ERR_UNSUPPORTED, "moe_layer_noalloc: this layer needs " + std::to_string(need) +
+                                          " bytes of scratch, more than the static array's " +
+                                          std::to_string(kScratchBytes) +
+                                          "; split the tokens or call lq_moe_layer with a workspace");
+  }
+  char *ws = nullptr;
+  int rc = scratch_on_current_device(&ws);
+  if (rc) return rc;
+  const hipStream_t st = as_stream(stream);
+  // the sync region must start zero; a call whose bounded wait gave up may
+  // have left it otherwise, so every call clears it first
+  const int words = static_cast<int>(lq_moe_sync_bytes() / sizeof(uint32_t));
+  zero_words_kernel<<<1, 256, 0, st>>>(reinterpret_cast<uint32_t *>(ws), words);
+  rc = check_launch("moe_layer_noalloc");
+  if (rc) return rc;
+  return lq_moe_layer(x, logits, logits_dtype, T, H, I, E, k, renormalize, q1, s1, q2, s2, bits, group_w1,
+                      group_w2, flags, ws, kScratchBytes, out, topk_ids_out, stream);
+}
+
 // K slices of the general GEMM for QuantLinear: with few row blocks the
 // items (block, 128-row slice) cannot fill the GPU, so each item also takes
 // one of S equal K slices (whole 128-wide chunks) and writes its partial sums

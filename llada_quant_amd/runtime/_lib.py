@@ -50,6 +50,8 @@ SIGNATURES = {
                               _P, _SZ, _P, _P]),
     "lq_moe_layer": (_I32, [_P, _P, _I32, _I64, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _I32, _I64, _I64,
                             _I32, _P, _SZ, _P, _P, _P]),
+    "lq_moe_layer_noalloc": (_I32, [_P, _P, _I32, _I64, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _I32, _I64,
+                                    _I64, _I32, _P, _P, _P]),
     "lq_moe_profile_events": (_I32, [_P, _I32]),
     "lq_moe_sync_bytes": (_SZ, []),
     "lq_moe_workspace_init": (_I32, [_P, _P]),

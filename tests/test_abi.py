@@ -201,3 +201,11 @@ def test_checkpoint_names_and_lookup(tmp_path):
     (tmp_path / "model-int8.safetensors").write_bytes(b"")
     with pytest.raises(RuntimeError, match="ambiguous"):
         find_weights_file(str(tmp_path))
+
+
+def test_no_alloc_layer_rejects_a_layer_beyond_its_static_array_on_the_host():
+    """lq_moe_layer_noalloc's scratch limit is checked before any device call."""
+    lib = _lib.load()
+    rc, msg = _rc_and_msg(lib.lq_moe_layer_noalloc(NULL, NULL, _lib.LQ_F32, 4096, 2048, 1024, 8, 8, 0, NULL, NULL,
+                                                   NULL, NULL, 4, 128, 128, 0, NULL, NULL, NULL))
+    assert rc == _lib.LQ_ERR_UNSUPPORTED and "scratch" in msg and "lq_moe_layer" in msg
