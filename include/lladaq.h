@@ -221,12 +221,12 @@ int lq_moe_status(const void *workspace, uint32_t *status, int clear,
  *   workspace of ws_bytes >= lq_moe_workspace_bytes(T, H, I, E, k)
  * Requires H % 128 == 0, I % 64 == 0, group lengths (after the per-row
  * fallback) that are multiples of 32, and T <= 262144.  Kernels on `stream`:
- * small layers of the streaming family (T*k <= 2048, exact weights) run as
- * ONE launch, the fused layer kernel (plan, GEMM1, GEMM2 and combine, the
+ * the expert plan, GEMM1, GEMM2, combine, with an x permute in front for the
+ * general and wide GEMMs.  With LQ_MOE_FUSED_LAYER, small layers of the
+ * streaming family (E <= 64, T*k <= 2048, exact weights) run as ONE launch
+ * instead, the fused layer kernel (plan, GEMM1, GEMM2 and combine, the
  * workgroups handing data to each other through the workspace's sync
- * region); otherwise the expert plan, GEMM1, GEMM2, combine, with an x
- * permute in front for the general and wide GEMMs.  No host
- * synchronisation.
+ * region).  No host synchronisation.
  */
 int lq_moe_forward(const void *x, int64_t T, int H, int I, int E, int k,
                    const int8_t *q1, const float *s1, const int8_t *q2,
