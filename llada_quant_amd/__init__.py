@@ -7,12 +7,16 @@ W4A16/W8A16 GEMMs with in-register bit-exact dequantization, fused SwiGLU and
 top-k combine, a bit-exact dequant kernel and a GPU MSE quantizer.
 
 The surface is the reference's: ``QuantConfig``, ``ExecutionMode.PACKED``,
-``quantize_model``, the ``block.w1`` property and
-``fused_moe(x, w1, w2, gating_output, topk_ids)``.
+``quantize_model``, the ``block.w1`` property,
+``fused_moe(x, w1, w2, gating_output, topk_ids)`` and the checkpoint format
+(``save_quantized_checkpoint`` / ``load_quantized_weights``, which reads the
+packed buffers straight into GPU memory).
 """
 
 from .api import QuantizationResult, TargetingError, quantize_model, quantized_model
 from .config import ExecutionMode, QuantConfig
+from .formats.manifest import QuantizationManifest
+from .formats.safetensors import load_quantized_weights, save_quantized_checkpoint
 from .runtime.fused_moe import fused_moe, fused_moe_packed, moe_layer
 from .runtime.moe import PackedExpertTensor
 from .runtime.routing import expert_token_stats, moe_permute, route_topk
@@ -23,7 +27,10 @@ __all__ = [
     "QuantConfig",
     "ExecutionMode",
     "QuantizationResult",
+    "QuantizationManifest",
     "TargetingError",
+    "save_quantized_checkpoint",
+    "load_quantized_weights",
     "quantize_model",
     "quantized_model",
     "fused_moe",

@@ -145,12 +145,14 @@ class ExpertTokenStats:
 
     @property
     def mean(self) -> float:
-        return sum(self.counts) / self.num_experts if self.num_experts else 0.0
+        """Rows per counted expert (0.0 for an empty histogram)."""
+        return sum(self.counts) / len(self.counts) if self.counts else 0.0
 
     @property
     def imbalance(self) -> float:
+        """Busiest expert's rows over the mean; 1.0 (balanced) when nothing was routed."""
         m = self.mean
-        return max(self.counts) / m if m else 0.0
+        return max(self.counts) / m if m else 1.0
 
     def percentile(self, p: float) -> float:
         ordered = sorted(self.counts)
@@ -160,16 +162,19 @@ class ExpertTokenStats:
         return float(ordered[idx])
 
     def to_dict(self) -> dict:
+        """The reference's report keys and rounding (analysis/moe_regime.py:186-199)."""
+        lo, hi = (min(self.counts), max(self.counts)) if self.counts else (0, 0)
         return {
             "tokens": self.tokens,
             "top_k": self.top_k,
             "num_experts": self.num_experts,
             "active_experts": self.active_experts,
-            "mean": self.mean,
+            "min": lo,
             "p50": self.percentile(50),
+            "mean": round(self.mean, 2),
             "p90": self.percentile(90),
             "p99": self.percentile(99),
-            "max": max(self.counts) if self.counts else 0,
+            "max": hi,
             "imbalance_max_over_mean": round(self.imbalance, 3),
         }
 

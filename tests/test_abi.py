@@ -186,23 +186,6 @@ def test_token_chunks_cover_calls_within_the_32bit_bounds():
     assert max_tokens_per_call(64, 64, 1) == 1 << 18
 
 
-def test_checkpoint_names_and_lookup(tmp_path):
-    """The reference's artifact layout: BF16 expert weights are derivable (never stored),
-    exactly one model-int*.safetensors per directory."""
-    from llada_quant_amd.checkpoint import derivable_tensor_names, find_weights_file, weights_filename
-
-    m = {"targets": [{"name": "layers.0.mlp", "kind": "expert"}, {"name": "layers.0.q_proj", "kind": "linear"}]}
-    assert derivable_tensor_names(m) == {"layers.0.mlp.w1", "layers.0.mlp.w2"}
-    assert weights_filename(4) == "model-int4.safetensors"
-    with pytest.raises(FileNotFoundError):
-        find_weights_file(str(tmp_path))
-    (tmp_path / "model-int4.safetensors").write_bytes(b"")
-    assert find_weights_file(str(tmp_path)).endswith("model-int4.safetensors")
-    (tmp_path / "model-int8.safetensors").write_bytes(b"")
-    with pytest.raises(RuntimeError, match="ambiguous"):
-        find_weights_file(str(tmp_path))
-
-
 def test_no_alloc_layer_rejects_a_layer_beyond_its_static_array_on_the_host():
     """lq_moe_layer_noalloc's scratch limit is checked before any device call."""
     lib = _lib.load()

@@ -14,7 +14,7 @@ import copy
 import pytest
 import torch
 
-from conftest import FusedExpertBlock, TinyMoEModel
+from conftest import ExpertMLP, ToyMoE
 from llada_quant_amd import ExecutionMode, PackedExpertTensor, QuantConfig, fused_moe, quantize_model
 from llada_quant_amd.adapters.llada_moe import (
     describe_fused_expert_block,
@@ -68,7 +68,7 @@ def test_reference_mode_keeps_parameters_and_matches_packed_values(expert_block)
 
 
 def test_quantization_is_reproducible(dev):
-    a, b = FusedExpertBlock().to(dev), FusedExpertBlock().to(dev)
+    a, b = ExpertMLP().to(dev), ExpertMLP().to(dev)
     quantize_llada_experts(a, _config())
     quantize_llada_experts(b, _config())
     for attr in ("_qw1", "_sw1", "_qw2", "_sw2"):
@@ -117,7 +117,7 @@ def test_quant_result_from_buffers_derives_the_group_size(dev):
 
 
 def test_expert_block_shape_reports_element_count(dev):
-    shape = describe_fused_expert_block(FusedExpertBlock().to(dev))
+    shape = describe_fused_expert_block(ExpertMLP().to(dev))
     assert shape.numel == 4 * (2 * 64 * 128 + 128 * 64)
     assert "E=4" in shape.describe()
 
@@ -142,8 +142,8 @@ def test_packed_weights_are_read_only(moe_model):
 
 def test_in_place_weight_loaders_are_blocked_in_packed_mode(moe_model):
     loaded = []
-    FusedExpertBlock.load_state_dict_from_unfused = lambda self, src: loaded.append(src)
-    moe_module._PACKED_CLASS_CACHE.clear()
+    ExpertMLP.load_state_dict_from_unfused = lambda self, src: loaded.append(src)
+    moe_module._PACKED_CLASSES.clear()
     try:
         moe_model.layers[0].mlp.load_state_dict_from_unfused("before")
         assert loaded == ["before"]
@@ -152,8 +152,8 @@ def test_in_place_weight_loaders_are_blocked_in_packed_mode(moe_model):
             moe_model.layers[0].mlp.load_state_dict_from_unfused("after")
         assert loaded == ["before"]
     finally:
-        del FusedExpertBlock.load_state_dict_from_unfused
-        moe_module._PACKED_CLASS_CACHE.clear()
+        del ExpertMLP.load_state_dict_from_unfused
+        moe_module._PACKED_CLASSES.clear()
 
 
 def test_int4_adapter_stores_packed_codes(moe_model):
@@ -211,6 +211,6 @@ def test_block_w1_feeds_fused_moe_without_a_bf16_copy(moe_model):
 
 def test_cpu_model_fails_loudly():
     """No CPU fallback: quantizing a CPU-resident model raises."""
-    model = TinyMoEModel()
+    model = ToyMoE()
     with pytest.raises(RuntimeError, match="GPU"):
         quantize_model(model, _config())

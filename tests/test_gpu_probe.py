@@ -37,7 +37,7 @@ def _codes(values: torch.Tensor, bits: int) -> torch.Tensor:
     return (lo | (hi << 4)).to(torch.uint8).to(torch.int8)
 
 
-def _layer(bits: int, H: int, I: int, seed: int, tiny_scales: bool):
+def _layer(bits: int, H: int, I: int, seed: int, scales: str):
     g = torch.Generator().manual_seed(seed)
     qmax = 7 if bits == 4 else 127
     # W1: gate rows all 1.0, up rows one-hot in K
@@ -49,10 +49,12 @@ def _layer(bits: int, H: int, I: int, seed: int, tiny_scales: bool):
     # W2: row 0 all 1.0; other rows random codes, scales over many binades
     c2 = torch.randint(-qmax - 1, qmax + 1, (1, H, I), generator=g, dtype=torch.int32)
     c2[0, 0, :] = 1
-    # down to 2^-100: every q*s and a*q*s stays a normal fp32 number, so the
-    # expected products below are exact
-    lo_exp = -100 if tiny_scales else -30
-    s2 = (2.0 ** torch.randint(lo_exp, 6, (1, H, 1), generator=g).float()) * (1 + torch.rand(1, H, 1, generator=g))
+    # "tiny": down to 2^-100; "huge": 2^103 .. 2^111, where the in-register
+    # dequant leaves its fast half-precision trick for the plain conversion
+    # (every such chunk); either way every q*s and a*q*s stays a normal fp32
+    # number, so the expected products below are exact
+    lo_exp, hi_exp = {"normal": (-30, 6), "tiny": (-100, 6), "huge": (103, 111)}[scales]
+    s2 = (2.0 ** torch.randint(lo_exp, hi_exp, (1, H, 1), generator=g).float()) * (1 + torch.rand(1, H, 1, generator=g))
     s2[0, 0, 0] = 1.0
     w1 = QuantResult(q=_codes(c1, bits), scale=s1, bits=bits, group_size=-1, packed=bits == 4,
                      logical_shape=(1, 2 * I, H))
@@ -68,10 +70,11 @@ def _to(r: QuantResult, dev) -> QuantResult:
 
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("T", [16, 32, 200])
-@pytest.mark.parametrize("tiny_scales", [False, True])
-def test_exact_layer_reproduces_standalone_dequant(dev, bits, T, tiny_scales):
+@pytest.mark.parametrize("scales", ["normal", "tiny", "huge"])
+def test_exact_layer_reproduces_standalone_dequant(dev, bits, T, scales):
+    """T=16 runs the streaming GEMMs, T=32 and 200 the wide ones."""
     H, I = 512, 512
-    w1, w2 = (_to(r, dev) for r in _layer(bits, H, I, seed=T + bits, tiny_scales=tiny_scales))
+    w1, w2 = (_to(r, dev) for r in _layer(bits, H, I, seed=T + bits, scales=scales))
     x = torch.eye(H, dtype=torch.bfloat16)[:T].to(dev)
     ids = torch.zeros(T, 1, dtype=torch.int32, device=dev)
     w = torch.ones(T, 1, device=dev)
