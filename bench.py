@@ -63,6 +63,8 @@ def parse_args():
     p.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0: enough to exceed 3x the MALL)")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="bound on the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-c3", action="store_true",
+                   help="c4: skip the large-token (C3) leg reported under the 'c3' key")
     p.add_argument("--no-gpu-baseline", action="store_true", help="skip the dequantize-then-GEMM leg")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--kernel", choices=("auto", "stream", "fused", "general", "wide"), default="auto",
@@ -493,16 +495,20 @@ def main():
     out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
     ids = torch.empty(T, k, dtype=torch.int32, device=dev)
 
-    def make_calls(flags):
+    def calls_for(xx, lg, renorm, ws, oo, ii, flags):
+        """lq_moe_layer argument tuples, one per weight copy, for tokens xx / logits lg."""
         calls = []
         for q1, q2 in layers:
-            g1, g2, _ = _check_weights(x, q1, q2)
+            g1, g2, _ = _check_weights(xx, q1, q2)
             calls.append((
-                _lib.ptr(x), _lib.ptr(logits), _lib.LQ_F32, T, H, I, E, k, int(cfg["renorm"]), _lib.ptr(q1.q),
+                _lib.ptr(xx), _lib.ptr(lg), _lib.LQ_F32, xx.shape[0], H, I, E, k, int(renorm), _lib.ptr(q1.q),
                 _lib.ptr(q1.scale), _lib.ptr(q2.q), _lib.ptr(q2.scale), cfg["bits"], g1, g2, flags,
-                _lib.ptr(workspace), ws_bytes, _lib.ptr(out), _lib.ptr(ids), ctypes.c_void_p(stream.cuda_stream),
+                _lib.ptr(ws), ws.numel(), _lib.ptr(oo), _lib.ptr(ii), ctypes.c_void_p(stream.cuda_stream),
             ))
         return calls
+
+    def make_calls(flags):
+        return calls_for(x, logits, cfg["renorm"], workspace, out, ids, flags)
 
     hip = Hip()
     hip.lib.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
@@ -629,6 +635,33 @@ def main():
     }
     if fused_extra is not None:
         result["fused_layer"] = fused_extra
+    if args.config == "c4" and not args.no_c3:
+        # the large-token regime on the same weights (C3 uses C4's INT4 MSE layer): 4096 tokens,
+        # unskewed routing, the wide (matrix-core) GEMMs; roofline of GEMM1 in TFLOP/s
+        c3 = CONFIGS["c3"]
+        T3 = c3["tokens"]
+        g3 = torch.Generator().manual_seed(args.seed + 13)
+        x3 = torch.randn(T3, H, generator=g3).to(torch.bfloat16).to(dev)
+        lg3 = torch.randn(T3, E, generator=g3).to(dev)
+        ws3 = _lib.moe_workspace(workspace_bytes(T3, H, I, E, k), dev)
+        out3 = torch.empty(T3, H, dtype=torch.bfloat16, device=dev)
+        ids3 = torch.empty(T3, k, dtype=torch.int32, device=dev)
+        calls3 = calls_for(x3, lg3, c3["renorm"], ws3, out3, ids3, 0)
+        ms3 = timed(calls3, max(10, args.steps // 4), 3)
+        st3 = staged(calls3, max(10, args.steps // 4))
+        flops1 = 2.0 * T3 * k * 2 * I * H
+        tf1 = flops1 / (st3[2] / 1e3) / 1e12
+        result["c3"] = {
+            "workload": f"C3: the same layer over {T3} tokens, top-{k}, unskewed routing",
+            "ms_per_step": round(ms3, 5), "value": round(T3 / (ms3 / 1e3), 1), "unit": "tokens/s",
+            "gemm_family": kernel_family(dict(cfg, tokens=T3, skew=False), False, "auto"),
+            "stage_ms": {name: round(v, 5) for name, v in zip(("route", "plan", "gemm1", "gemm2", "combine"), st3)},
+            "layer_tflops": round(2.0 * T3 * k * 3 * I * H / (ms3 / 1e3) / 1e12, 1),
+            "roofline": {"kernel": KERNEL_NAMES["wide"], "bound": "mfma", "achieved": round(tf1, 1),
+                         "peak": MI355X_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(tf1 / MI355X_BF16_TFLOPS, 4),
+                         "algorithmic_flops": flops1, "avg_ms": round(st3[2], 5)},
+        }
+        del ws3, x3, out3
     if not args.no_gpu_baseline:
         result["gpu_dequant_then_gemm"] = gpu_dequant_then_gemm(torch, cfg, layers, x, logits,
                                                                 max(5, args.steps // 10), 3)

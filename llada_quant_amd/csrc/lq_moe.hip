@@ -3064,15 +3064,47 @@ int linear_wide_ksplit(int64_t M, int K, int N) {
   return S;
 }
 
+// Workspace of a QuantLinear call: the one-expert plan (offsets, sorted
+// rows, row blocks of 32 or 128 rows), the S slots of every row (ids 0,
+// weights 1), x in K-slot order [M, K] bf16 and the S partial sums of every
+// output [M, S, N] fp32.  S is the larger of the two families' K-slice counts,
+// so one size serves either family.
+struct LinLayout {
+  size_t offsets, sorted, srow, hdr, blocks, ids, weights, act, ybuf, total;
+  int S;
+};
+
+LinLayout lin_layout(int64_t M, int K, int N) {
+  LinLayout w;
+  w.S = std::max(linear_ksplit(M, K, N), K % (2 * kKC) == 0 ? linear_wide_ksplit(M, K, N) : 1);
+  const int64_t slots = M * w.S;
+  size_t off = 0;
+  auto take = [&](size_t &field, size_t bytes) {
+    field = off;
+    off = align256(off + bytes);
+  };
+  take(w.offsets, sizeof(int32_t) * 2);
+  take(w.sorted, sizeof(int32_t) * M);
+  take(w.srow, sizeof(int32_t) * M);
+  take(w.hdr, sizeof(PlanHeader));
+  take(w.blocks, sizeof(int4) * std::max<int64_t>(1, ceil_div(M, kRowsMax)));
+  take(w.ids, sizeof(int32_t) * slots);
+  take(w.weights, sizeof(float) * slots);
+  take(w.act, sizeof(uint16_t) * M * K);
+  take(w.ybuf, sizeof(float) * slots * N);
+  w.total = off;
+  return w;
+}
+
 // QuantLinear (runtime/linear.py:127-131): out = bf16(x . dequant(W)^T) with
 // fp32 accumulation, W [N, K] packed INT4 / INT8 with fp32 group scales
 // along K -- the layer's second GEMM with one expert, top-1, weight 1.0:
-// set-up (x into K-slot order, ids 0, weights 1), plan, GEMM2 (wide when its
-// items fill the GPU, else general with K slices), combine.
+// set-up (x into K-slot order, ids 0, weights 1, and the one-expert plan),
+// GEMM2 (the wide family from 128 rows on, else the general one; both split
+// K into slices until about 512 items exist), combine.
 extern "C" size_t lq_linear_workspace_bytes(int64_t M, int K, int N) {
   if (M < 0 || K <= 0 || N <= 0) return 0;
-  return ws_layout(M, N, K, 1, std::max(linear_ksplit(M, K, N), K % (2 * kKC) == 0 ? linear_wide_ksplit(M, K, N) : 1))
-      .total;
+  return lin_layout(M, K, N).total;
 }
 
 extern "C" int lq_quant_linear(const void *x, int64_t M, int K, int N, const int8_t *q, const float *s, int bits,
@@ -3104,8 +3136,7 @@ extern "C" int lq_quant_linear(const void *x, int64_t M, int K, int N, const int
     return fail(LQ_ERR_VALUE, "quant_linear: x, qweight, workspace and out must be 16-byte aligned");
   const bool wide = linear_wide(M, K, N, flags);
   const int S = wide ? linear_wide_ksplit(M, K, N) : linear_ksplit(M, K, N);
-  const WsLayout w = ws_layout(
-      M, N, K, 1, std::max(linear_ksplit(M, K, N), K % (2 * kKC) == 0 ? linear_wide_ksplit(M, K, N) : 1));
+  const LinLayout w = lin_layout(M, K, N);
   if (ws_bytes < w.total)
     return fail(LQ_ERR_VALUE, "quant_linear: workspace too small (" + std::to_string(ws_bytes) + " < " +
                                   std::to_string(w.total) + ")");
@@ -3114,7 +3145,17 @@ extern "C" int lq_quant_linear(const void *x, int64_t M, int K, int N, const int
   float *weights = reinterpret_cast<float *>(ws + w.weights);
   uint16_t *act = reinterpret_cast<uint16_t *>(ws + w.act);
   const int64_t n8 = M * K / 8;
-  PlanArgs p = plan_args(ids, M, 1, 1, ws, w);
+  PlanArgs p;
+  p.ids = ids;
+  p.N = M;
+  p.E = 1;
+  p.k = 1;
+  p.counts = nullptr;
+  p.offsets = reinterpret_cast<int32_t *>(ws + w.offsets);
+  p.sorted = reinterpret_cast<int32_t *>(ws + w.sorted);
+  p.srow = reinterpret_cast<int32_t *>(ws + w.srow);
+  p.blocks = reinterpret_cast<int4 *>(ws + w.blocks);
+  p.hdr = reinterpret_cast<PlanHeader *>(ws + w.hdr);
   p.block_rows = wide ? kWRows : kRowsMax;
   linear_setup_kernel<<<static_cast<int>(ceil_div(std::max(n8, M * S), 256)), 256, 0, st>>>(
       static_cast<const uint16_t *>(x), n8, M, M * S, act, ids, weights, p.sorted, p.srow, p.blocks, p.hdr,

@@ -39,8 +39,8 @@ def quant_linear(
     """``bf16(x . W^T)`` for packed ``W`` (``[..., in] -> [..., out]``), fp32 accumulation.
 
     ``wide_kernel`` / ``general_kernel`` force one GEMM family (the same bits;
-    for comparison): rows >= 32 take the wide kernels by themselves where
-    ``out % 256 == 0`` and ``in % 256 == 0``.
+    for comparison): by themselves, 128 rows or more take the wide kernels
+    where ``out % 256 == 0`` and ``in % 256 == 0``, fewer the general ones.
     """
     if bits not in (8, 4):
         raise ValueError(f"bits must be 8 or 4, got {bits}")

@@ -42,6 +42,8 @@ def rel(out: torch.Tensor, truth: torch.Tensor) -> float:
     (300, 1024, 768, 4, 128),
     (16, 512, 256, 8, -1),     # one group per row
     (2, 8192, 512, 4, 128),    # long K: 16 K slices per item
+    (160, 1536, 256, 8, 512),  # wide, 2 K slices: the slice boundary at K=768 falls inside group 1
+    (200, 1024, 512, 4, 64),   # wide with per-lane scales (two groups per 128-wide chunk)
 ])
 def test_quant_linear_matches_truth_and_blas(dev, M, K, N, bits, group):
     g = torch.Generator().manual_seed(M + K + N)
