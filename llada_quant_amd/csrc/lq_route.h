@@ -7,25 +7,16 @@ namespace lq {
 
 constexpr int kMaxExperts = 256;
 
-// Route one token with one wavefront from its logits v (lane l holds experts
-// l, l+64, ...: EPL of them; lanes past E hold -inf): fp32 softmax over the
-// E logits, top-k by rank counting.  Each expert's rank is rank(e) =
-// #{e' : x[e'] > x[e], or x[e'] == x[e] and e' < e} over the token's logits
-// (broadcast lane by lane), so ids come out in descending-logit order with
-// ties to the lower expert id -- the order of descending probability,
-// softmax being monotone -- with no serial selection rounds.  Experts of
-// rank < k call put(rank, e, p) with their fp32 softmax probability p
-// (renormalized over the k when renorm).  Restates
-// softmax(logits, -1, dtype=float32).topk(k) of trajectory/llada.py:228-234.
-// Routing of one token over E <= 64 experts (lane e = expert e; lanes past E
-// hold -inf), the cheap way.  softmax as route_values below.  The top-k set is found by a radix select on orderable
-// 32-bit keys of the logits (-0.0 taken as +0.0, so equal logits have equal
-// keys; lanes past E key 0, below every logit): 32 ballots of key >= c
-// build the k-th largest key from the top bit down; the set is every key
-// above it plus the lowest-numbered lanes equal to it.  Each selected lane's
-// rank is then counted against the k selected ones only: (greater key) or
-// (equal key and lower expert id).  The ids, their order and the weights
-// are those of the rank count in route_values.
+// Routing of one token over E <= 64 experts with one wavefront (lane e holds
+// expert e's logit v; lanes past E hold -inf): fp32 softmax as route_values
+// below.  The top-k set comes from a radix select on orderable 32-bit keys
+// of the logits (-0.0 keyed as +0.0, so equal logits have equal keys; lanes
+// past E key 0, below every logit): 32 ballots of key >= c build the k-th
+// largest key from the top bit down, and the set is every key above it plus
+// the lowest-numbered lanes equal to it.  Each selected lane's rank is then
+// counted against the k selected ones only: (greater key) or (equal key and
+// lower expert id).  The ids, their order and the weights are those of the
+// rank count in route_values.
 template <class Put>
 __device__ __forceinline__ void route_values64(float v, int E, int k, int renorm, Put put) {
   const int lane = threadIdx.x & 63;
@@ -60,6 +51,17 @@ __device__ __forceinline__ void route_values64(float v, int E, int k, int renorm
   if (mine) put(rank, lane, renorm ? pw / wsum : pw);
 }
 
+// Route one token with one wavefront from its logits v (lane l holds experts
+// l, l+64, ...: EPL of them; lanes past E hold -inf): fp32 softmax over the
+// E logits, top-k by rank counting.  Each expert's rank is rank(e) =
+// #{e' : x[e'] > x[e], or x[e'] == x[e] and e' < e} over the token's logits
+// (broadcast lane by lane), so ids come out in descending-logit order with
+// ties to the lower expert id -- the order of descending probability,
+// softmax being monotone -- with no serial selection rounds.  Experts of
+// rank < k call put(rank, e, p) with their fp32 softmax probability p
+// (renormalized over the k when renorm).  Restates
+// softmax(logits, -1, dtype=float32).topk(k) of trajectory/llada.py:228-234.
+// One logit per lane (EPL == 1) takes route_values64.
 template <int EPL, class Put>
 __device__ __forceinline__ void route_values(const float (&v)[EPL], int E, int k, int renorm, Put put) {
   if constexpr (EPL == 1) {
