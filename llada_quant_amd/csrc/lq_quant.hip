@@ -155,43 +155,72 @@ __device__ __forceinline__ float candidate_ratio(double max_shrink, int step, in
   return static_cast<float>(1.0 - max_shrink * static_cast<double>(step) / static_cast<double>(grid));
 }
 
-// The IEEE quotient RN(x / s) from y = RN(1 / s), computed once per candidate
-// scale (Markstein's division): q0 = RN(x y); r = x - s q is exact with an
-// FMA; after one correction q1 = RN(q0 + r0 y) lies within one ulp of x / s,
-// and then RN(q1 + r1 y) is the correctly rounded quotient.  That holds
-// without underflow or overflow, so the caller takes it only for a normal,
-// finite s with a normal reciprocal and |x| >= 2^-100 or x = 0 (the
-// quotients of a group are bounded by 2 Qmax, the residuals then stay
-// normal); other lanes divide.
-struct RecipScale {
-  float s, y;
-  bool ok;  // the Markstein quotient applies for this scale
+// Code of x for scale s: clamp(rint(RN(x / s)), qmin, qmax), rint rounding
+// half to even.  Only the integer rint(RN(x / s)) matters, so no quotient is
+// rounded correctly unless it has to be.  Once per scale of a group whose
+// largest magnitude is amax: y ~ 1/s (the hardware reciprocal and one Newton
+// step, relative error <= 2^-23) and Q = RN(amax y), which no |q0| of the
+// group exceeds.  Per weight: q0 = RN(x y) and r = rint(q0).
+//
+// Bound: with s and 1/s normal, |q0 - x/s| + |RN(x/s) - x/s| <= |q0| 2^-21 +
+// 2^-148.  The weight keeps r when |q0 - r| (exact) < t = RN(0.5 - Q 2^-18):
+// then q0 lies more than Q 2^-18 - 2^-26 >= |q0| 2^-18 - 2^-26 from the
+// nearest half-integer, above that bound for |q0| >= 2^-7, and below that
+// 0.5 - |q0| > 0.49 dominates it; so RN(x/s) lies in the same open interval
+// (r - 1/2, r + 1/2) as q0 and rounds to r as well.  Otherwise (near a
+// half-integer, a non-finite q0, t <= 0 once Q >= 2^17) the weight divides.
+// Scales outside [2^-100, 2^126] always divide (t = -1); from 2^-100 up a
+// subnormal x has |x/s| < 2^-26 and code 0 whether the product flushes it or
+// not.  The clamp of a kept r, finite and below 2^17, is one v_med3.
+struct QuotScale {
+  float s, y, t;
 };
-__device__ __forceinline__ RecipScale recip_scale(float s) {
-  const float y = 1.0f / s;
-  const bool ok = s >= 0x1p-126f && s <= 0x1p125f && y >= 0x1p-126f;
-  return {s, y, ok};
+__device__ __forceinline__ QuotScale quot_scale(float s, float amax) {
+  const float y0 = __builtin_amdgcn_rcpf(s);
+  const float y = fmaf(fmaf(-s, y0, 1.0f), y0, y0);
+  const bool fast = s >= 0x1p-100f && s <= 0x1p126f;
+  return {s, y, fast ? fmaf(amax * y, -0x1p-18f, 0.5f) : -1.0f};
 }
-__device__ __forceinline__ float div_rs(float x, const RecipScale &d) {
-  float q;
-  if (d.ok && (x == 0.0f || fabsf(x) >= 0x1p-100f)) {
-    const float q0 = x * d.y;
-    const float q1 = fmaf(fmaf(-q0, d.s, x), d.y, q0);
-    q = fmaf(fmaf(-q1, d.s, x), d.y, q1);
-  } else {
-    q = x / d.s;
-  }
-  return q;
+// The code from the product alone; sets redo when the weight must divide
+// (the code returned is then meaningless).
+__device__ __forceinline__ float quot_code_fast(float x, const QuotScale &d, float qmin, float qmax, bool &redo) {
+  const float q0 = x * d.y;
+  const float r = rintf(q0);
+  redo |= !(fabsf(q0 - r) < d.t);
+  return __builtin_amdgcn_fmed3f(r, qmin, qmax);
+}
+__device__ __forceinline__ float quot_code_div(float x, const QuotScale &d, float qmin, float qmax) {
+  return fminf(fmaxf(rintf(x / d.s), qmin), qmax);
+}
+// code from quot_code_fast, replaced by the division's where that applies
+__device__ __forceinline__ float quot_code_fix(float x, const QuotScale &d, float qmin, float qmax, float code) {
+  bool redo = false;
+  quot_code_fast(x, d, qmin, qmax, redo);
+  return redo ? quot_code_div(x, d, qmin, qmax) : code;
+}
+__device__ __forceinline__ float quot_code(float x, const QuotScale &d, float qmin, float qmax) {
+  bool redo = false;
+  const float c = quot_code_fast(x, d, qmin, qmax, redo);
+  return redo ? quot_code_div(x, d, qmin, qmax) : c;
 }
 
-__device__ __forceinline__ float sq_err(float x, const RecipScale &d, float qmin, float qmax) {
-  const float safe = d.s;
-  float v = div_rs(x, d);                // work = wf / safe
-  v = rintf(v);                          // round_ (half to even)
-  v = fminf(fmaxf(v, qmin), qmax);       // clamp_
-  v = v * safe;                          // mul_(safe)
-  v = v - x;                             // sub_(wf)
-  return v * v;                          // pow_(2)
+// the reference's squared error of one weight, from its code
+__device__ __forceinline__ float sq_err_code(float x, float code, float safe) {
+  float v = code * safe;  // mul_(safe)
+  v = v - x;              // sub_(wf)
+  return v * v;           // pow_(2)
+}
+__device__ __forceinline__ float sq_err(float x, const QuotScale &d, float qmin, float qmax) {
+  // (wf / safe).round_().clamp_(qmin, qmax)
+  return sq_err_code(x, quot_code(x, d, qmin, qmax), d.s);
+}
+
+// Lane 8j of a row of 16 gets p of lane 8j + N (row_shl:N; N <= 7 stays
+// inside the row).  Other lanes get values they do not use.
+template <int N>
+__device__ __forceinline__ float row_shl(float p) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, p), 0x100 | N, 0xF, 0xF,
+                                                               false));
 }
 
 __device__ __forceinline__ float round_scale(float v, int sdt) {
@@ -234,13 +263,14 @@ struct QuantArgs {
 //   acc[k] = sum over rows r of e[(4r + k)*8 + l]      (k = 0..3)
 //   acc[0] += tail vectors;  p = ((acc0 + acc1) + acc2) + acc3
 //   err = 0 + (((0 + p_0) + p_1) + ... + p_7)
-template <int WDT, int MAXV>
+// EXACT: n is exactly 8 * MAXV, so every vector test below folds away.
+template <int WDT, int MAXV, bool EXACT>
 __global__ __launch_bounds__(kBlock) void quant_group8_kernel(QuantArgs a) {
   const int lane = threadIdx.x & 63;
   const int l8 = lane & 7;
   const int64_t gi = gtid() >> 3;
   const bool active = gi < a.n_groups;
-  const int vs = static_cast<int>(a.n >> 3);
+  const int vs = EXACT ? MAXV : static_cast<int>(a.n >> 3);
   const int64_t base = (active ? gi : 0) * a.n;
   const float qmax = static_cast<float>((1 << (a.bits - 1)) - 1);
   const float qmin = -static_cast<float>(1 << (a.bits - 1));
@@ -261,17 +291,34 @@ __global__ __launch_bounds__(kBlock) void quant_group8_kernel(QuantArgs a) {
   float chosen = amax_s;
   if (a.mse) {
     const int rows4 = (vs >> 2) << 2;
+    // candidate ratios of steps 0..63, one per lane, read back by step
+    const float lane_ratio = candidate_ratio(a.max_shrink, lane, a.grid);
     float best = amax_s;
     float best_err = __builtin_inff();
     for (int step = 0; step < a.grid; ++step) {
-      const float cand = amax_s * candidate_ratio(a.max_shrink, step, a.grid);
+      const float ratio =
+          step < 64 ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lane_ratio), step))
+                    : candidate_ratio(a.max_shrink, step, a.grid);
+      const float cand = amax_s * ratio;
       const float safe = cand > 0.0f ? cand : 1.0f;
-      const RecipScale rs = recip_scale(safe);
+      const QuotScale rs = quot_scale(safe, m);
+      // codes from the products; a lane with a quotient too near a
+      // half-integer (rare) then redoes those weights by division
+      float code[MAXV];
+      bool redo = false;
+#pragma unroll
+      for (int i = 0; i < MAXV; ++i)
+        if (i < vs) code[i] = quot_code_fast(x[i], rs, qmin, qmax, redo);
+      if (redo) {
+#pragma unroll
+        for (int i = 0; i < MAXV; ++i)
+          if (i < vs) code[i] = quot_code_fix(x[i], rs, qmin, qmax, code[i]);
+      }
       float acc0 = 0.0f, acc1 = 0.0f, acc2 = 0.0f, acc3 = 0.0f;
 #pragma unroll
       for (int i = 0; i < MAXV; ++i) {
         if (i < vs) {
-          const float e = sq_err(x[i], rs, qmin, qmax);
+          const float e = sq_err_code(x[i], code[i], safe);
           if (i < rows4) {
             if ((i & 3) == 0) acc0 += e;
             else if ((i & 3) == 1) acc1 += e;
@@ -283,16 +330,23 @@ __global__ __launch_bounds__(kBlock) void quant_group8_kernel(QuantArgs a) {
         }
       }
       const float p = ((acc0 + acc1) + acc2) + acc3;
-      float f = 0.0f;
-      const int g0 = lane & ~7;
-#pragma unroll
-      for (int l = 0; l < 8; ++l) f += __shfl(p, g0 + l, 64);
+      // the group's first lane adds the 8 partials in lane order; the
+      // other lanes' err and best are never used
+      float f = 0.0f + p;
+      f += row_shl<1>(p);
+      f += row_shl<2>(p);
+      f += row_shl<3>(p);
+      f += row_shl<4>(p);
+      f += row_shl<5>(p);
+      f += row_shl<6>(p);
+      f += row_shl<7>(p);
       const float err = 0.0f + f;
       if (err < best_err) {
         best_err = err;
         best = cand;
       }
     }
+    best = __shfl(best, lane & ~7, 64);
     chosen = amax_s > 0.0f ? best : 0.0f;
   }
 
@@ -300,13 +354,11 @@ __global__ __launch_bounds__(kBlock) void quant_group8_kernel(QuantArgs a) {
   if (active && l8 == 0) store_scale(a.scale, gi, stored, a.scale_dtype);
   if (!a.write_q) return;
 
-  const float safe = stored > 0.0f ? stored : 1.0f;
+  const QuotScale qs = quot_scale(stored > 0.0f ? stored : 1.0f, m);
 #pragma unroll
   for (int i = 0; i < MAXV; ++i) {
     if (i < vs) {
-      float v = rintf(x[i] / safe);
-      v = fminf(fmaxf(v, qmin), qmax);
-      const int qi = static_cast<int>(v);
+      const int qi = static_cast<int>(quot_code(x[i], qs, qmin, qmax));
       const int64_t e = base + 8 * i + l8;
       if (!a.pack) {
         if (active) a.q[e] = static_cast<int8_t>(qi);
@@ -413,7 +465,7 @@ __global__ __launch_bounds__(kBlock) void quant_generic_kernel(QuantArgs a) {
     for (int step = 0; step < a.grid; ++step) {
       const float cand = amax_s * candidate_ratio(a.max_shrink, step, a.grid);
       const float safe = cand > 0.0f ? cand : 1.0f;
-      const RecipScale rs = recip_scale(safe);
+      const QuotScale rs = quot_scale(safe, m);
       auto err = [&](int64_t i) { return sq_err(load_f32<WDT>(a.w, base + i), rs, qmin, qmax); };
       const float e = torch_cpu_sum(err, a.n);
       if (e < best_err) {
@@ -451,12 +503,20 @@ int launch_quant(const QuantArgs &a, int w_dtype, hipStream_t st) {
     if (a.n_groups * 8 > static_cast<int64_t>(grid) * kBlock)
       return fail(LQ_ERR_UNSUPPORTED, "quantize: too many groups for one launch");
     LQ_DISPATCH_DTYPE(w_dtype, WDT, {
-      if (vs <= 4)
-        quant_group8_kernel<WDT, 4><<<grid, kBlock, 0, st>>>(a);
-      else if (vs <= 16)
-        quant_group8_kernel<WDT, 16><<<grid, kBlock, 0, st>>>(a);
+      if (vs == 4)
+        quant_group8_kernel<WDT, 4, true><<<grid, kBlock, 0, st>>>(a);
+      else if (vs == 8)
+        quant_group8_kernel<WDT, 8, true><<<grid, kBlock, 0, st>>>(a);
+      else if (vs == 16)
+        quant_group8_kernel<WDT, 16, true><<<grid, kBlock, 0, st>>>(a);
+      else if (vs == 32)
+        quant_group8_kernel<WDT, 32, true><<<grid, kBlock, 0, st>>>(a);
+      else if (vs < 4)
+        quant_group8_kernel<WDT, 4, false><<<grid, kBlock, 0, st>>>(a);
+      else if (vs < 16)
+        quant_group8_kernel<WDT, 16, false><<<grid, kBlock, 0, st>>>(a);
       else
-        quant_group8_kernel<WDT, 32><<<grid, kBlock, 0, st>>>(a);
+        quant_group8_kernel<WDT, 32, false><<<grid, kBlock, 0, st>>>(a);
     });
   } else {
     const int grid = grid_1d(a.n_groups, kBlock);

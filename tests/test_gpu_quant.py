@@ -226,3 +226,29 @@ def test_mse_search_extreme_magnitudes_match_the_oracle(dev, bits, group):
     oq, os_, _ = O.quantize(w, bits, group, "mse", grid=16, w_dtype=O.F32)
     assert np.array_equal(res.scale.cpu().numpy(), os_)
     assert np.array_equal(res.q.cpu().numpy(), oq)
+
+
+@pytest.mark.parametrize("bits,grid", [(4, 16), (8, 16), (4, 80)])
+def test_mse_search_quotients_near_half_integers_match_the_oracle(dev, bits, grid):
+    """Weights within 3 ulps of (m + 1/2) times one of the group's candidate scales: the
+    MSE search's quotient shortcut must hand those to the IEEE division, and still agree
+    with the oracle bit for bit.  Grid 80 also takes the candidate ratios past step 63,
+    which the kernel computes per step instead of reading them from a lane."""
+    rng = np.random.default_rng(11 * bits + grid)
+    qmax = 2 ** (bits - 1) - 1
+    groups, group = 384, 128
+    amax = rng.uniform(0.01, 0.05, size=groups).astype(np.float32)
+    amax_s = amax / np.float32(qmax)  # fp32 quotient, as the search forms it
+    steps = rng.integers(0, grid, size=(groups, group))
+    ratio = (1.0 - 0.5 * steps / grid).astype(np.float32)
+    cand = amax_s[:, None] * ratio  # fp32 products: the candidate scales
+    m = rng.integers(-qmax, qmax, size=(groups, group))  # |m + 1/2| <= qmax - 1/2 keeps |w| < amax
+    near = ((m + 0.5) * cand.astype(np.float64)).astype(np.float32)
+    w = (near.view(np.int32) + rng.integers(-3, 4, size=near.shape).astype(np.int32)).view(np.float32)
+    w[:, 0] = amax * np.where(rng.random(groups) < 0.5, -1, 1).astype(np.float32)
+    w = w.reshape(groups // 4, 4 * group)
+    res = quantize_tensor(torch.from_numpy(w).to(dev), bits=bits, group_size=group, scale_search="mse",
+                          search_grid=grid)
+    oq, os_, _ = O.quantize(w, bits, group, "mse", grid=grid, w_dtype=O.F32)
+    assert np.array_equal(res.scale.cpu().numpy(), os_)
+    assert np.array_equal(res.q.cpu().numpy(), oq)
