@@ -142,10 +142,15 @@ def moe_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
 
     The library's MoE calls need the sync region at the start of their
     workspace zero on entry and leave it zero, so a workspace allocated here
-    serves any number of later calls (one stream at a time).
+    serves any number of later calls (one stream at a time).  Only that
+    region is cleared (a fill kernel, no memset node under graph capture): the
+    rest is scratch every call overwrites, and a C5-sized layer's workspace
+    is about 1 GB.
     """
-    n = max(int(nbytes), int(load().lq_moe_sync_bytes()), 1)
-    return torch.zeros(n, dtype=torch.uint8, device=device)
+    sync = int(load().lq_moe_sync_bytes())
+    ws = torch.empty(max(int(nbytes), sync, 1), dtype=torch.uint8, device=device)
+    ws[:sync].zero_()
+    return ws
 
 
 def check_status(workspace: torch.Tensor, what: str) -> None:
