@@ -115,7 +115,7 @@ def pmc_traffic(config, form, kernel="gemm1"):
 
 KERNEL_NAMES = {
     "fused": "moe_fused_kernel (route + plan + GEMM1 + GEMM2 + combine in one launch, W1/W2 streamed per CU)",
-    "wide": "moe_wide_kernel<G1> (blocks of <= 128 rows, 4 weight tiles x 8 row tiles per wave, SwiGLU epilogue)",
+    "wide": "moe_wide_kernel<G1> (blocks of <= 128 rows, 2 weight tiles x 8 row tiles per wave, SwiGLU epilogue)",
     "stream": "moe_stream_kernel<G1> (W1 gate and up tiles streamed per CU)",
     "general": "moe_gemm_kernel<G1> (W1 gate+up, SwiGLU epilogue; persistent)",
 }
