@@ -819,8 +819,9 @@ __device__ __forceinline__ void wide_item(const MoeArgs &a, int e, int slice, in
 #pragma unroll
     for (int c = 0; c < NT; ++c) tot[rt][c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
   // Schedule (loads of a wave complete in issue order):
-  //   first:    the item's scales, for the dequant choice (below)
-  //   prologue: tokens 0 -> LDS stage 0, weights 0; tokens 1 -> registers, weights 1
+  //   first:    the item's scales, for the dequant choice (below), then
+  //             tokens 0 and weights 0, which do not depend on the choice
+  //   prologue: tokens 0 -> LDS stage 0; tokens 1 -> registers, weights 1
   //   step i:   compute chunk i (weights slot i & 1, LDS stage i & 1);
   //             tokens i+1: registers -> LDS stage (i+1) & 1 (waits for them only:
   //             weights i+1 were issued after them); issue tokens i+2 and
@@ -845,34 +846,39 @@ __device__ __forceinline__ void wide_item(const MoeArgs &a, int e, int slice, in
   // (the groups of this item's K range [c0, c0 + nk) chunks: [g0, g1))
   const int g0 = c0 * kKC / G, g1 = min(ng, ((c0 + nk) * kKC + G - 1) / G);
   bool ok = g1 - g0 <= 4 * kChk;
+  float chk[NT][kChk];
   {
+    // groups past the range read as 0 (fast) through an out-of-range offset,
+    // so the descriptor stays uniform
     const __amdgpu_buffer_rsrc_t rs = ok ? srsrc : empty;
-    float chk[NT][kChk];
 #pragma unroll
     for (int c = 0; c < NT; ++c)
 #pragma unroll
-      for (int j = 0; j < kChk; ++j)  // groups past the range read as 0 (fast)
+      for (int j = 0; j < kChk; ++j)
         chk[c][j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                  g0 + lg + 4 * j < g1 ? rs : empty, svoff[c], 4 * (g0 + lg + 4 * j), 0));
-#pragma unroll
-    for (int c = 0; c < NT; ++c)
-#pragma unroll
-      for (int j = 0; j < kChk; ++j) ok = ok && dq_fast_ok(chk[c][j]);
+                                                  rs, g0 + lg + 4 * j < g1 ? svoff[c] + 4 * (g0 + lg + 4 * j) : kOutOfRange,
+                                                  0, 0));
   }
-  // prologue and K loop, one copy per dequant form
+  // chunk 0's loads do not depend on the dequant form: they go out behind
+  // the scale checks, so the choice waits for the checks only
+  WChunk<BITS> wb[2][NT];
+  float sb[2][NT];
+  u32x4 av[NQ];
+  if constexpr (!FIRST) {
+    if (tid < rows) wt_r = a.topk_w[asg_r];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  load_a(0, av);
+  __builtin_amdgcn_sched_barrier(0);
+  load_w(0, wb[0], sb[0]);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int c = 0; c < NT; ++c)
+#pragma unroll
+    for (int j = 0; j < kChk; ++j) ok = ok && dq_fast_ok(chk[c][j]);
+  // the rest of the prologue and the K loop, one copy per dequant form
   auto kloop = [&](auto fast_tag) __attribute__((always_inline)) {
     constexpr bool FAST = decltype(fast_tag)::value;
-    WChunk<BITS> wb[2][NT];
-    float sb[2][NT];
-    u32x4 av[NQ];
-    if constexpr (!FIRST) {
-      if (tid < rows) wt_r = a.topk_w[asg_r];
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    load_a(0, av);
-    __builtin_amdgcn_sched_barrier(0);
-    load_w(0, wb[0], sb[0]);
-    __builtin_amdgcn_sched_barrier(0);
     if constexpr (!FIRST) {
       if (tid < rows) {
         r_asg[tid] = asg_r;
@@ -968,7 +974,10 @@ __global__ __launch_bounds__(kWThreads, 1) void moe_wide_kernel(MoeArgs a) {
     const int rem = t - blk * per;
     const int slice = rem / ksplit;
     const int ks = rem - slice * ksplit;
-    const int4 bi = a.blocks[blk];
+    // a scalar load: the block table was written by an earlier launch
+    typedef int i32x4 __attribute__((ext_vector_type(4)));
+    const i32x4 bi = *reinterpret_cast<const __attribute__((address_space(4))) i32x4 *>(
+        reinterpret_cast<uintptr_t>(a.blocks + blk));
     const int e = __builtin_amdgcn_readfirstlane(bi.x);
     const int row0 = __builtin_amdgcn_readfirstlane(bi.y);
     const int rows = __builtin_amdgcn_readfirstlane(bi.z);
