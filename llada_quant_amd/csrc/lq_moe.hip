@@ -109,7 +109,8 @@ struct MoeArgs {
   int4 *slotplan;          // streaming, in-kernel plan: per CU slot {expert, first row, rows, i << 16 | m}
   int32_t *slotasg;        // ... and the assignment of each of its block's rows [slot][kRowsMax]
   uint16_t *act;           // [T*k, I] bf16, by sorted row
-  float *ybuf;             // [T*k, H] fp32, by assignment
+  float *ybuf;             // QuantLinear: [M*ksplit, N] fp32 K-slice partial sums (MoE layers: unused)
+  uint16_t *ybf;           // MoE layers: [T*k, H] bf16 slot outputs by assignment (QuantLinear: nullptr)
   uint16_t *out;           // [T, H] bf16
   int64_t T;
   int H, I, E, k;
@@ -537,9 +538,15 @@ __device__ __forceinline__ void gemm_item(const MoeArgs &a, int e, int slice, in
         if (m < rows) {
           const int asg = a.sorted[row0 + m];
           const float wt = a.topk_w[asg];
-          float *yrow = a.ybuf + (static_cast<int64_t>(asg) * ksplit + ks) * a.H;
-          yrow[wr[0]] = tot[rt][0][j] * wt;
-          yrow[wr[1]] = tot[rt][1][j] * wt;
+          if (a.ybf) {  // MoE slot output, rounded to bf16 (ksplit is 1)
+            uint16_t *yrow = a.ybf + static_cast<int64_t>(asg) * a.H;
+            yrow[wr[0]] = static_cast<uint16_t>(cvt2(tot[rt][0][j] * wt, 0.0f));
+            yrow[wr[1]] = static_cast<uint16_t>(cvt2(tot[rt][1][j] * wt, 0.0f));
+          } else {
+            float *yrow = a.ybuf + (static_cast<int64_t>(asg) * ksplit + ks) * a.H;
+            yrow[wr[0]] = tot[rt][0][j] * wt;
+            yrow[wr[1]] = tot[rt][1][j] * wt;
+          }
         }
       }
   }
@@ -555,11 +562,14 @@ __device__ __forceinline__ void gemm_dispatch(const MoeArgs &a, int e, int slice
 }
 
 // out[t, h..h+2) = bf16(sum_j y[t*k + j, h..h+2)) over the routed slots, j
-// ascending (2 outputs per thread: enough threads to cover every CU).  The
-// slot ids and slot outputs of a run of 8 slots are loaded together -- one
-// memory round trip -- and the outputs of slots whose id is out of range
-// (never written) are left out of the sum.
-__global__ __launch_bounds__(kCombineBlock) void combine_kernel(const float *__restrict__ ybuf,
+// ascending, summed in fp32 (2 outputs per thread: enough threads to cover
+// every CU).  BF: the slot outputs are bf16 (MoE layers), else fp32
+// (QuantLinear's K-slice partial sums).  The slot ids and slot outputs of a
+// run of 8 slots are loaded together -- one memory round trip -- and the
+// outputs of slots whose id is out of range (never written) are left out of
+// the sum.
+template <bool BF>
+__global__ __launch_bounds__(kCombineBlock) void combine_kernel(const void *__restrict__ ybuf,
                                                                 const int32_t *__restrict__ ids, int64_t T,
                                                                 int H, int k, int E, uint16_t *__restrict__ out) {
   const int64_t base = (static_cast<int64_t>(blockIdx.x) * kCombineBlock + threadIdx.x) * 2;
@@ -567,7 +577,7 @@ __global__ __launch_bounds__(kCombineBlock) void combine_kernel(const float *__r
   const int64_t t = base / H;
   const int h = static_cast<int>(base - t * H);
   const int32_t *idr = ids + t * k;
-  const float *yr = ybuf + t * k * H + h;
+  const int64_t y0 = t * k * H + h;  // element offset of slot 0's pair
   float s0 = 0.0f, s1 = 0.0f;
   for (int j0 = 0; j0 < k; j0 += 8) {
     int id[8];
@@ -576,7 +586,13 @@ __global__ __launch_bounds__(kCombineBlock) void combine_kernel(const float *__r
     for (int jj = 0; jj < 8; ++jj) {
       const int j = j0 + jj < k ? j0 + jj : k - 1;
       id[jj] = idr[j];
-      v[jj] = *reinterpret_cast<const float2 *>(yr + static_cast<int64_t>(j) * H);
+      const int64_t off = y0 + static_cast<int64_t>(j) * H;
+      if constexpr (BF) {
+        const uint32_t p = *reinterpret_cast<const uint32_t *>(static_cast<const uint16_t *>(ybuf) + off);
+        v[jj] = make_float2(__uint_as_float(p << 16), __uint_as_float(p & 0xFFFF0000u));
+      } else {
+        v[jj] = *reinterpret_cast<const float2 *>(static_cast<const float *>(ybuf) + off);
+      }
     }
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj) {
@@ -936,9 +952,15 @@ __device__ __forceinline__ void wide_item(const MoeArgs &a, int e, int slice, in
         if (m < rows) {
           const int asg = r_asg[m];
           const float wt = r_wt[m];
-          float *yrow = a.ybuf + (static_cast<int64_t>(asg) * ksplit + ks) * a.H + obase + lc;
+          if (a.ybf) {  // MoE slot output, rounded to bf16 (ksplit is 1)
+            uint16_t *yrow = a.ybf + static_cast<int64_t>(asg) * a.H + obase + lc;
 #pragma unroll
-          for (int c = 0; c < NT; ++c) yrow[16 * c] = tot[rt][c][j] * wt;
+            for (int c = 0; c < NT; ++c) yrow[16 * c] = static_cast<uint16_t>(cvt2(tot[rt][c][j] * wt, 0.0f));
+          } else {
+            float *yrow = a.ybuf + (static_cast<int64_t>(asg) * ksplit + ks) * a.H + obase + lc;
+#pragma unroll
+            for (int c = 0; c < NT; ++c) yrow[16 * c] = tot[rt][c][j] * wt;
+          }
         }
       }
   }
@@ -1360,11 +1382,12 @@ __device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, 
             else
               a.act[eoff[rt][j] + 16 * u] = h;
           } else {
-            const float y = tot[rt][0][j] * ewt[rt][j];
+            // slot output y * w, rounded to bf16 (the streaming kernels run MoE layers only)
+            const uint16_t y = static_cast<uint16_t>(cvt2(tot[rt][0][j] * ewt[rt][j], 0.0f));
             if constexpr (COH)
-              __hip_atomic_store(a.ybuf + eoff[rt][j] + 16 * u, y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              __hip_atomic_store(a.ybf + eoff[rt][j] + 16 * u, y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             else
-              a.ybuf[eoff[rt][j] + 16 * u] = y;
+              a.ybf[eoff[rt][j] + 16 * u] = y;
           }
         }
       }
@@ -1843,16 +1866,17 @@ __device__ __forceinline__ void compact_rows(const uint16_t *ids_l, int N, int k
 }
 
 // Slice blockIdx.x of the layer's combine: out[t, h..h+4) = bf16(sum_j y[t*k +
-// j, h..h+4)) over the slots with a valid id, j ascending (combine_kernel's
-// sums), y read with sc1 loads (other workgroups wrote it in this launch).
-// Slots without a valid id were never written and are left out; with routing
+// j, h..h+4)) over the slots with a valid id, j ascending, the bf16 slot
+// outputs summed in fp32 (combine_kernel's sums), y read with sc1 loads
+// (other workgroups wrote it in this launch).  Slots without a valid id were never written and are left out; with routing
 // in-kernel every id is valid.
 __device__ __forceinline__ void fused_combine(const MoeArgs &a, bool route) {
   const int k = a.k, H = a.H;
   const int64_t nq = a.T * H / 4;  // 4 outputs per task
   const int64_t q0 = nq * blockIdx.x / gridDim.x, q1 = nq * (blockIdx.x + 1) / gridDim.x;
-  // (the host bounds T*k*H*4 below 2^31: 32-bit byte offsets)
-  const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.ybuf, a.T * k * H * 4);
+  // (the host bounds T*k*H*4 below 2^31: 32-bit byte offsets); bf16 slot outputs
+  const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.ybf, a.T * k * H * 2);
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
   for (int64_t q = q0 + threadIdx.x; q < q1; q += kSThreads) {
     const int64_t t = q / (H / 4);
     const int h = static_cast<int>(q - t * (H / 4)) * 4;
@@ -1860,19 +1884,21 @@ __device__ __forceinline__ void fused_combine(const MoeArgs &a, bool route) {
     for (int j0 = 0; j0 < k; j0 += 8) {
       // up to 8 slots' loads in flight at once; slots past k or without a
       // valid id read the token's first slot and are not added
-      floatx4 v[8];
+      u32x2 v[8];
       bool ok[8];
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) {
         const int j = j0 + jj;
         const int id = j < k ? (route ? 0 : a.ids[t * k + j]) : -1;
         ok[jj] = id >= 0 && id < a.E;
-        const int off = static_cast<int>(((t * k + (ok[jj] ? j : 0)) * H + h) * 4);
-        v[jj] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(yr, off, 0, kCpolSc1));
+        const int off = static_cast<int>(((t * k + (ok[jj] ? j : 0)) * H + h) * 2);
+        v[jj] = __builtin_amdgcn_raw_buffer_load_b64(yr, off, 0, kCpolSc1);
       }
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj)
-        if (ok[jj]) s += v[jj];
+        if (ok[jj])
+          s += floatx4{__uint_as_float(v[jj][0] << 16), __uint_as_float(v[jj][0] & 0xFFFF0000u),
+                       __uint_as_float(v[jj][1] << 16), __uint_as_float(v[jj][1] & 0xFFFF0000u)};
     }
     uint2 o;
     o.x = static_cast<uint32_t>(f32_to_bf16_bits(s[0])) | (static_cast<uint32_t>(f32_to_bf16_bits(s[1])) << 16);
@@ -2364,7 +2390,7 @@ WsLayout ws_layout(int64_t T, int H, int I, int E, int k) {
   take(w.weights, sizeof(float) * N);
   take(w.xperm, sizeof(uint16_t) * T * H);
   take(w.act, sizeof(uint16_t) * N * 2 * I);  // act [N, I] (general) or gate/up [N, 2I] (streaming)
-  take(w.ybuf, sizeof(float) * N * H);
+  take(w.ybuf, sizeof(uint16_t) * N * H);  // bf16 slot outputs
   w.total = off;
   return w;
 }
@@ -2694,8 +2720,8 @@ int launch_phases(const MoeArgs &a, int64_t max_g1, int64_t max_g2, hipStream_t 
     if (rc) return rc;
   }
   const int64_t n2 = a.T * a.H / 2;
-  combine_kernel<<<static_cast<int>(ceil_div(n2, kCombineBlock)), kCombineBlock, 0, st>>>(a.ybuf, a.ids, a.T, a.H,
-                                                                                          a.k, a.E, a.out);
+  combine_kernel<true><<<static_cast<int>(ceil_div(n2, kCombineBlock)), kCombineBlock, 0, st>>>(a.ybf, a.ids, a.T,
+                                                                                                a.H, a.k, a.E, a.out);
   const int rc = check_launch("moe_combine");
   if (rc) return rc;
   pm.mark(first + 3);
@@ -2766,7 +2792,8 @@ MoeArgs layer_args(const void *x, int64_t T, int H, int I, int E, int k, const i
   a.slotplan = reinterpret_cast<int4 *>(ws + w.slotplan);
   a.slotasg = reinterpret_cast<int32_t *>(ws + w.slotasg);
   a.act = reinterpret_cast<uint16_t *>(ws + w.act);
-  a.ybuf = reinterpret_cast<float *>(ws + w.ybuf);
+  a.ybuf = nullptr;  // (QuantLinear's fp32 partial sums)
+  a.ybf = reinterpret_cast<uint16_t *>(ws + w.ybuf);
   a.out = static_cast<uint16_t *>(out);
   a.T = T;
   a.H = H;
@@ -2985,8 +3012,9 @@ namespace lq {
 
 // Each GPU the library runs on holds its own copy of this array from the
 // code object's load to the end of the process.  64 MiB covers every layer
-// whose per-assignment buffers fit: T*k*H*4 (the fp32 partial outputs) is the
-// largest term, 32 MiB at T*k = 4096 with H = 2048.
+// whose per-assignment buffers fit: the gate / up rows (T*k*2I*2 bytes) and
+// the bf16 slot outputs (T*k*H*2) are the largest terms, 16 MiB each at
+// T*k = 4096 with H = 2048, I = 1024.
 constexpr size_t kScratchBytes = size_t{64} << 20;
 static __device__ __align__(256) char scratch[kScratchBytes];
 
@@ -3229,7 +3257,7 @@ extern "C" int lq_quant_linear(const void *x, int64_t M, int K, int N, const int
   rc = check_launch("quant_linear_gemm");
   if (rc) return rc;
   const int64_t n2 = M * N / 2;
-  combine_kernel<<<static_cast<int>(ceil_div(n2, kCombineBlock)), kCombineBlock, 0, st>>>(a.ybuf, ids, M, N, S, 1,
-                                                                                          a.out);
+  combine_kernel<false><<<static_cast<int>(ceil_div(n2, kCombineBlock)), kCombineBlock, 0, st>>>(a.ybuf, ids, M, N,
+                                                                                                 S, 1, a.out);
   return check_launch("quant_linear_combine");
 }
