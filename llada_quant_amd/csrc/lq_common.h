@@ -155,12 +155,12 @@ __device__ __forceinline__ float half_hi_f32(uint32_t v) {
 
 // 8 INT4 codes of one dword (element i in nibble i) -> e[i] = fp32(q_i) * s
 __device__ __forceinline__ void dq_int4x8(uint32_t w, const DqScale &d, float (&e)[8]) {
-  const uint32_t v = w ^ 0x88888888u;
-  const uint32_t vs = v >> 8;
-  const uint32_t t0 = v & 0x000F000Fu;   // n0, n4
-  const uint32_t t1 = v & 0x00F000F0u;   // 16 n1, 16 n5
-  const uint32_t t2 = vs & 0x000F000Fu;  // n2, n6
-  const uint32_t t3 = vs & 0x00F000F0u;  // 16 n3, 16 n7
+  // each (x ^ c) & m is one v_bitop3_b32; the shift is the only other op
+  const uint32_t ws = w >> 8;
+  const uint32_t t0 = (w ^ 0x00080008u) & 0x000F000Fu;   // n0, n4
+  const uint32_t t1 = (w ^ 0x00800080u) & 0x00F000F0u;   // 16 n1, 16 n5
+  const uint32_t t2 = (ws ^ 0x00080008u) & 0x000F000Fu;  // n2, n6
+  const uint32_t t3 = (ws ^ 0x00800080u) & 0x00F000F0u;  // 16 n3, 16 n7
   e[0] = fmaf(half_lo_f32(t0), d.s24, d.c);
   e[4] = fmaf(half_hi_f32(t0), d.s24, d.c);
   e[1] = fmaf(half_lo_f32(t1), d.s20, d.c);
@@ -173,9 +173,8 @@ __device__ __forceinline__ void dq_int4x8(uint32_t w, const DqScale &d, float (&
 
 // 4 INT8 codes of one dword (element i in byte i) -> e[i] = fp32(q_i) * s
 __device__ __forceinline__ void dq_int8x4(uint32_t w, const DqScale &d, float (&e)[4]) {
-  const uint32_t v = w ^ 0x80808080u;
-  const uint32_t t0 = v & 0x00FF00FFu;         // n0, n2
-  const uint32_t t1 = (v >> 8) & 0x00FF00FFu;  // n1, n3
+  const uint32_t t0 = (w ^ 0x00800080u) & 0x00FF00FFu;         // n0, n2 (one v_bitop3_b32)
+  const uint32_t t1 = ((w >> 8) ^ 0x00800080u) & 0x00FF00FFu;  // n1, n3
   e[0] = fmaf(half_lo_f32(t0), d.s24, d.c);
   e[2] = fmaf(half_hi_f32(t0), d.s24, d.c);
   e[1] = fmaf(half_lo_f32(t1), d.s24, d.c);
