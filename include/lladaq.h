@@ -296,12 +296,16 @@ int lq_moe_profile_events(void *const *events, int n_events);
  *   q [N, K] int8 or [N, K/2] packed INT4, s [N, K/G] f32 (group = -1 or
  *   K % group != 0: one group per row).
  * Requires N % 128 == 0, K % 64 == 0, group length % 32 == 0, M <= 262144.
- * flags: 0, LQ_MOE_WIDE_KERNEL or LQ_MOE_GENERAL_KERNEL (same results).  The
- * bias of the reference module is added by the caller (a bf16 add after the
- * bf16 product, as the reference does).  Kernels on `stream`: set-up (which
- * also writes the one-expert plan), GEMM (the wide family from 128 rows on,
- * else the general one; both may split K into slices), combine; no host
- * synchronisation, no device allocation.
+ * flags: 0, LQ_MOE_WIDE_KERNEL or LQ_MOE_GENERAL_KERNEL (each deterministic;
+ * the families may differ in summation order).  The bias of the reference
+ * module is added by the caller (a bf16 add after the bf16 product, as the
+ * reference does).  Kernels on `stream`: with flags 0 and up to 16 rows (32
+ * when K splits into at most 8 slices) one kernel that sums the general
+ * family's K slices in its order (the general family's bits; the workspace
+ * is not touched); otherwise set-up (which also writes the one-expert plan),
+ * GEMM (the wide family from 128 rows on, else the general one; both may
+ * split K into slices), combine.  No host synchronisation, no device
+ * allocation.
  */
 int lq_quant_linear(const void *x, int64_t M, int K, int N, const int8_t *q,
                     const float *s, int bits, int64_t group, int flags,

@@ -2338,6 +2338,134 @@ __global__ __launch_bounds__(256) void linear_setup_kernel(const uint16_t *__res
 }
 
 // ---------------------------------------------------------------------------
+// QuantLinear for a few rows (M <= 32), one launch: out = bf16(x . W^T).
+//
+// Workgroup b owns output columns [32 b, 32 b + 32) -- two 16-row tiles of
+// W -- and has S waves; wave ks sums the chunks of K slice ks (nks whole
+// 128-wide chunks), the slices the general GEMM2 + combine path uses for the
+// same shape.  Each wave streams its two tiles' codes and scales (kD chunks
+// in flight) and reads its A fragments straight from x in natural order (x
+// is small and stays in L2; each fragment feeds both tiles), permuting each
+// 8-value piece into the K-slot order in registers; the per-chunk arithmetic
+// is chunk_mfma_f's.  The S partial tiles meet in LDS and are added in
+// ascending slice order from 0.0f, as the combine adds the general path's
+// slots, then rounded once to bf16 -- so the two paths agree bit for bit.
+// Rows of x past M read zeros (offsets past the buffer's end) and are never
+// stored.
+// ---------------------------------------------------------------------------
+struct LinArgs {
+  const uint16_t *x;  // [M, K] bf16
+  const int8_t *q;    // [N, K] int8 or [N, K/2] packed
+  const float *s;     // [N, ng]
+  uint16_t *out;      // [M, N] bf16
+  int M, K, N;
+  int G, ng;          // group length along K (a multiple of 32) and groups per row
+  int nks;            // chunks per K slice (a multiple of the kernel's KD)
+};
+
+constexpr int kLinNT = 2;          // 16-row weight tiles per workgroup
+constexpr int kLinMaxSlices = 16;  // linear_ksplit's cap
+
+template <int BITS, int NRT, int KD, int MAXS>
+__global__ __launch_bounds__(64 * MAXS) void linear_small_kernel(LinArgs a) {
+  constexpr int NT = kLinNT;
+  constexpr int kElems = NRT * 4 * NT * 64;  // one partial of the workgroup's tiles
+  __shared__ float part[MAXS][kElems];
+  const int tid = threadIdx.x;
+  const int ks = __builtin_amdgcn_readfirstlane(tid >> 6);  // this wave's K slice
+  const int S = static_cast<int>(blockDim.x >> 6);
+  const int lane = tid & 63;
+  const int lc = lane & 15;
+  const int lg = lane >> 4;
+  const int n0 = 16 * NT * static_cast<int>(blockIdx.x);
+  constexpr int kLaneBytes = BITS == 4 ? 16 : 32;  // one lane's 32 codes of a chunk
+  constexpr int kChunkBytes = BITS == 4 ? 64 : 128;
+  const int rowbytes = BITS == 4 ? (a.K >> 1) : a.K;
+  const int c_first = ks * a.nks;
+  const __amdgpu_buffer_rsrc_t wrsrc = make_rsrc(a.q + static_cast<int64_t>(n0) * rowbytes, 16ll * NT * rowbytes);
+  const __amdgpu_buffer_rsrc_t srsrc = make_rsrc(a.s + static_cast<int64_t>(n0) * a.ng, 16ll * NT * a.ng * 4);
+  const int64_t xbytes = static_cast<int64_t>(a.M) * a.K * 2;  // below 2^31 (host-checked)
+  const __amdgpu_buffer_rsrc_t xrsrc = make_rsrc(a.x, xbytes);
+  const __amdgpu_buffer_rsrc_t empty = make_rsrc(a.out, 0);  // reads zeros, no memory traffic
+  const int wvoff = lc * rowbytes + kLaneBytes * lg;  // tile c adds 16 c rows
+  const int svoff = lc * a.ng * 4;
+  int xoff[NRT];  // row 16 rt + lc, K offset 32 lg of each chunk; rows past M read zeros
+#pragma unroll
+  for (int rt = 0; rt < NRT; ++rt) {
+    const int m = 16 * rt + lc;
+    xoff[rt] = m < a.M ? m * a.K * 2 + 64 * lg : static_cast<int>(xbytes);
+  }
+
+  WChunk<BITS> wb[KD][NT];
+  float sb[KD][NT];
+  uint4 xb[KD][NRT][4];
+  // chunk i of this slice into ring slot d (the loads stay in flight); past
+  // the slice's end every load goes through the empty descriptor, so each
+  // step issues the same loads and the wait counts stay exact
+  auto load = [&](int i, int d) __attribute__((always_inline)) {
+    const bool live = i < a.nks;
+    const int c = c_first + (live ? i : 0);
+    const __amdgpu_buffer_rsrc_t rw = live ? wrsrc : empty, rs = live ? srsrc : empty, rx = live ? xrsrc : empty;
+    // the group of this lane's 32 codes (G is a multiple of 32, so they share it)
+    const int sidx = (c * kKC + 32 * lg) / a.G;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int vo = wvoff + 16 * t * rowbytes;
+      if constexpr (BITS == 4) {
+        wb[d][t].v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vo, c * kChunkBytes, 0));
+      } else {
+        wb[d][t].v0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vo, c * kChunkBytes, 0));
+        wb[d][t].v1 =
+            __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vo + 16, c * kChunkBytes, 0));
+      }
+      sb[d][t] = __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(rs, svoff + 16 * t * a.ng * 4 + 4 * sidx, 0, 0));
+    }
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+        xb[d][rt][p] = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, xoff[rt] + 16 * p, c * kKC * 2, 0));
+  };
+
+  floatx4 tot[NRT][NT];
+#pragma unroll
+  for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) tot[rt][t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int d = 0; d < KD; ++d) load(d, d);
+  for (int i0 = 0; i0 < a.nks; i0 += KD) {
+#pragma unroll
+    for (int d = 0; d < KD; ++d) {
+      // A fragment of step s: K piece 4 lg + s of the chunk, in K-slot order
+      auto afrag = [&](int rt, int s) __attribute__((always_inline)) { return permute_kslots(xb[d][rt][s]); };
+      if (__all(dq_fast_ok(sb[d][0]) && dq_fast_ok(sb[d][1])))
+        chunk_mfma_f<BITS, false, true, NRT, NT>(wb[d], sb[d], afrag, tot);
+      else
+        chunk_mfma_f<BITS, false, false, NRT, NT>(wb[d], sb[d], afrag, tot);
+      load(i0 + d + KD, d);  // the chunk KD ahead
+    }
+  }
+  // partial element ((rt * 4 + j) * NT + t) * 64 + lane
+#pragma unroll
+  for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) part[ks][((rt * 4 + j) * NT + t) * 64 + lane] = tot[rt][t][j];
+  __syncthreads();
+  for (int e = tid; e < kElems; e += static_cast<int>(blockDim.x)) {
+    float acc = 0.0f;  // the combine's order: 0, then the slots by ascending slice
+    for (int u = 0; u < S; ++u) acc += part[u][e];
+    const int l = e & 63, t = (e >> 6) % NT, rj = (e >> 6) / NT;  // rj = rt * 4 + j
+    const int m = 16 * (rj >> 2) + 4 * (l >> 4) + (rj & 3);
+    if (m < a.M) a.out[static_cast<int64_t>(m) * a.N + n0 + 16 * t + (l & 15)] = f32_to_bf16_bits(acc);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 
@@ -3103,6 +3231,15 @@ bool linear_wide(int64_t M, int K, int N, int flags) {
   return wide_eligible(N, K, 0) && M >= kWRows;
 }
 
+// a few rows without a forced family take the one-launch small kernel (its
+// waves are the general path's K slices, at most kLinMaxSlices of them; two
+// row tiles fit its registers with up to 8 slices)
+bool linear_small(int64_t M, int K, int N, int flags) {
+  if (flags & (LQ_MOE_WIDE_KERNEL | LQ_MOE_GENERAL_KERNEL)) return false;
+  if (M < 1 || K % kKC != 0) return false;
+  return M <= 16 || (M <= 32 && linear_ksplit(M, K, N) <= 8);
+}
+
 int linear_wide_ksplit(int64_t M, int K, int N) {
   const int64_t items = ceil_div(M, kWRows) * (N / kWR2);
   const int npair = K / (2 * kKC);
@@ -3187,6 +3324,47 @@ extern "C" int lq_quant_linear(const void *x, int64_t M, int K, int N, const int
   if (ws_bytes < w.total)
     return fail(LQ_ERR_VALUE, "quant_linear: workspace too small (" + std::to_string(ws_bytes) + " < " +
                                   std::to_string(w.total) + ")");
+  if (linear_small(M, K, N, flags)) {
+    // one launch: each workgroup sums the general path's S K slices of two
+    // 16-column tiles itself (no set-up, no workspace, no combine)
+    LinArgs la;
+    la.x = static_cast<const uint16_t *>(x);
+    la.q = q;
+    la.s = s;
+    la.out = static_cast<uint16_t *>(out);
+    la.M = static_cast<int>(M);
+    la.K = K;
+    la.N = N;
+    la.G = static_cast<int>(g);
+    la.ng = static_cast<int>(K / g);
+    la.nks = K / kKC / S;
+    const dim3 grid(static_cast<unsigned>(N / (16 * kLinNT))), block(static_cast<unsigned>(64 * S));
+    const bool two = M > 16;
+    // chunks in flight per wave: 4 for one row tile with up to 8 waves (256
+    // registers each), else 2 (two row tiles take linear_small only with up
+    // to 8 waves: with 16, 128 registers do not hold them)
+    const int kd = S <= 8 && !two ? (la.nks % 4 == 0 ? 4 : la.nks % 2 == 0 ? 2 : 1) : (la.nks % 2 == 0 ? 2 : 1);
+#define LQ_LIN_SMALL(B)                                                                        \
+  do {                                                                                         \
+    if (two) {                                                                                 \
+      if (kd == 2) linear_small_kernel<B, 2, 2, 8><<<grid, block, 0, st>>>(la);                \
+      else linear_small_kernel<B, 2, 1, 8><<<grid, block, 0, st>>>(la);                        \
+    } else if (S <= 8) {                                                                       \
+      if (kd == 4) linear_small_kernel<B, 1, 4, 8><<<grid, block, 0, st>>>(la);                \
+      else if (kd == 2) linear_small_kernel<B, 1, 2, 8><<<grid, block, 0, st>>>(la);           \
+      else linear_small_kernel<B, 1, 1, 8><<<grid, block, 0, st>>>(la);                        \
+    } else {                                                                                   \
+      if (kd == 2) linear_small_kernel<B, 1, 2, kLinMaxSlices><<<grid, block, 0, st>>>(la);    \
+      else linear_small_kernel<B, 1, 1, kLinMaxSlices><<<grid, block, 0, st>>>(la);            \
+    }                                                                                          \
+  } while (0)
+    if (bits == 4)
+      LQ_LIN_SMALL(4);
+    else
+      LQ_LIN_SMALL(8);
+#undef LQ_LIN_SMALL
+    return check_launch("quant_linear_small");
+  }
   char *ws = static_cast<char *>(workspace);
   int32_t *ids = reinterpret_cast<int32_t *>(ws + w.ids);
   float *weights = reinterpret_cast<float *>(ws + w.weights);

@@ -38,9 +38,11 @@ def quant_linear(
 ) -> torch.Tensor:
     """``bf16(x . W^T)`` for packed ``W`` (``[..., in] -> [..., out]``), fp32 accumulation.
 
-    ``wide_kernel`` / ``general_kernel`` force one GEMM family (the same bits;
-    for comparison): by themselves, 128 rows or more take the wide kernels
-    where ``out % 256 == 0`` and ``in % 256 == 0``, fewer the general ones.
+    ``wide_kernel`` / ``general_kernel`` force one GEMM family (for
+    comparison; each is deterministic): by themselves, 128 rows or more take
+    the wide kernels where ``out % 256 == 0`` and ``in % 256 == 0``, up to 16
+    rows (32 with at most 8 K slices) a one-launch kernel with the general
+    family's bits, and the rows between the general family.
     """
     if bits not in (8, 4):
         raise ValueError(f"bits must be 8 or 4, got {bits}")

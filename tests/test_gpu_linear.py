@@ -67,6 +67,30 @@ def test_quant_linear_matches_truth_and_blas(dev, M, K, N, bits, group):
     assert torch.equal(out, quant_linear(x, q.q, q.scale, bits, group))  # deterministic
 
 
+@pytest.mark.parametrize("M,K,N,bits,group", [
+    (1, 8192, 512, 8, 128),    # 16 K slices of 4 chunks (16 waves, 2 chunks in flight)
+    (16, 8192, 8192, 4, 128),  # the benchmark's shape: 8 slices of 8 chunks (4 in flight)
+    (5, 2048, 256, 8, 64),     # per-lane scales, 16 slices of one chunk
+    (17, 1024, 384, 4, 32),    # two row tiles, the second with one row
+    (20, 2048, 8192, 8, 128),  # two row tiles, 8 slices of 2 chunks
+    (32, 1024, 256, 8, -1),    # two full row tiles, one group per row
+    (9, 1152, 128, 4, 128),    # 9 chunks: odd, one K slice
+    (32, 4096, 256, 8, 128),   # 16 slices with two row tiles: the general path itself
+])
+def test_small_linear_matches_the_general_path_bit_for_bit(dev, M, K, N, bits, group):
+    """Up to 16 rows (32 with at most 8 K slices) take the one-launch kernel, which sums the
+    general path's K slices in its order."""
+    g = torch.Generator().manual_seed(7 * M + K + N)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    q = quantize_tensor(w, bits=bits, group_size=group)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+    out = quant_linear(x, q.q, q.scale, bits, group)
+    ref = quant_linear(x, q.q, q.scale, bits, group, general_kernel=True)
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    truth = x.double().cpu() @ oracle_weight(q).t()
+    assert rel(out, truth) < 3e-3
+
+
 def test_quant_linear_module_from_linear(dev):
     """QuantLinear.from_linear + forward with bias, leading batch dims, storage bytes."""
     torch.manual_seed(3)
