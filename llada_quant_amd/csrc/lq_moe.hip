@@ -650,7 +650,7 @@ __global__ __launch_bounds__(kThreads, 3) void moe_gemm_kernel(MoeArgs a) {
 // rows [32w, 32w + 32) of the slice (256 per item) -- and multiplies each
 // dequantized B fragment with up to 8 row tiles staged in LDS.  One
 // dequantization then feeds 128 rows instead of 32, which keeps the weight
-// arithmetic (~18 VALU per 8 weights, 4 cycles each) below the matrix-core
+// arithmetic (17 VALU per 8 weights, 4 cycles each) below the matrix-core
 // time of the fragment (8 x v_mfma_f32_16x16x32_bf16, 16 cycles each).
 // Token rows are staged one 128-wide K chunk at a time by all 512 threads
 // (double buffered, 32 KB per stage, one barrier per chunk), one chunk
@@ -700,7 +700,7 @@ __device__ __forceinline__ void wide_chunk(const WChunk<BITS> (&w)[NT], const fl
       a[rt] = *reinterpret_cast<const uint4 *>(buf + (rt * 16 + lc) * kRowBytes + 16 * ((4 * lg + s) ^ lds_swizzle(lc)));
   };
   // VALU instructions to place after each MFMA (the dequant of one step is
-  // ~18 per tile)
+  // 17 (INT4) or 18 (INT8) per tile)
   constexpr int kValuPer = (18 * NT + NRT * NT - 1) / (NRT * NT);
   auto step = [&](int s, const uint4(&ac)[NRT], const uint4(&bc)[NT], uint4(&an)[NRT], uint4(&bn)[NT])
                   __attribute__((always_inline)) {
