@@ -353,8 +353,8 @@ def bench_c5(args, torch):
     end to end together with the GPU quantize+pack (MSE scale search, 16 clip ratios in
     [0.5, 1.0], group 128) of every layer's BF16 weights.  Each layer is
     h <- h + moe_layer(h) (a residual keeps the activations at unit scale through the
-    stack; the add is inside the timed region).  Layers run as two token chunks of 16384
-    (one library call addresses T*k*H*4 < 2^31 bytes)."""
+    stack; the add is inside the timed region).  Each layer is one library call over all
+    32768 tokens (262144 assignments)."""
     from llada_quant_amd.algorithms.symmetric import quantize_tensor
     from llada_quant_amd.runtime.fused_moe import _chunks, max_tokens_per_call, moe_layer
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))

@@ -1349,7 +1349,7 @@ __device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, 
   for (int rt = 0; rt < NRT; ++rt) tot[rt][0] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
   // epilogue targets of this lane's rows m = rt*16 + 4*lg + j (32-bit
-  // element offsets: the host bounds T*k*max(H, I)*4 below 2^31): G1 writes
+  // element offsets: the host bounds T*k*max(2I, H)*2 below 2^31): G1 writes
   // row row0 + m of the gate / up pre-activations, G2 the slot output of
   // assignment rasg[m] scaled by its routing weight
   const int ld = FIRST ? 2 * a.I : a.H;
@@ -1874,7 +1874,7 @@ __device__ __forceinline__ void fused_combine(const MoeArgs &a, bool route) {
   const int k = a.k, H = a.H;
   const int64_t nq = a.T * H / 4;  // 4 outputs per task
   const int64_t q0 = nq * blockIdx.x / gridDim.x, q1 = nq * (blockIdx.x + 1) / gridDim.x;
-  // (the host bounds T*k*H*4 below 2^31: 32-bit byte offsets); bf16 slot outputs
+  // (the host bounds T*k*H*2 below 2^31: 32-bit byte offsets); bf16 slot outputs
   const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.ybf, a.T * k * H * 2);
   typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
   for (int64_t q = q0 + threadIdx.x; q < q1; q += kSThreads) {
@@ -2613,9 +2613,11 @@ int validate_layer(const void *x, int64_t T, int H, int I, int E, int k, const i
                 "moe_forward: the group length along K must be a multiple of 32 (got " + std::to_string(g1) +
                     " for w1, " + std::to_string(g2) + " for w2)");
   const int64_t N = T * k;
-  // the GEMMs address x, act, one expert's codes and one expert's scales
-  // through 32-bit buffer offsets below kOutOfRange
-  if (T > (int64_t{1} << 18) || N * static_cast<int64_t>(H > I ? H : I) * 4 > 0x7FFFFFFFll ||
+  // the GEMMs address x, the bf16 gate / up rows [N, 2I] and slot outputs
+  // [N, H], one expert's codes and one expert's scales through 32-bit
+  // offsets (bytes below kOutOfRange; element offsets into those buffers
+  // below 2^30)
+  if (T > (int64_t{1} << 18) || N * static_cast<int64_t>(2 * I > H ? 2 * I : H) * 2 > 0x7FFFFFFFll ||
       T * static_cast<int64_t>(H) * 2 >= kOutOfRange)
     return fail(LQ_ERR_UNSUPPORTED, "moe_forward: too many tokens for one call");
   if (int64_t{2} * I * H >= kOutOfRange)

@@ -124,13 +124,14 @@ def fused_moe_packed(
 def max_tokens_per_call(H: int, I: int, top_k: int) -> int:
     """Largest token count one library call takes.
 
-    The kernels address the per-assignment buffers and x with 32-bit buffer
-    offsets: T*k*max(H, I)*4 must stay below 2^31, T*H*2 below the buffer
-    descriptor range, and T <= 2^18.  Larger inputs are split into token
-    chunks by fused_moe_packed and moe_layer (a token's output depends only
-    on its own row and routing, so the split is exact).
+    The kernels address the per-assignment buffers (bf16 gate / up rows
+    [T*k, 2I] and slot outputs [T*k, H]) and x with 32-bit offsets:
+    T*k*max(2I, H)*2 must stay below 2^31, T*H*2 below the buffer descriptor
+    range, and T <= 2^18.  Larger inputs are split into token chunks by
+    fused_moe_packed and moe_layer (a token's output depends only on its own
+    row and routing, so the split is exact).
     """
-    lim = min((2**31 - 1) // (top_k * max(H, I) * 4), (0x7FFFFFF0 - 1) // (H * 2), 1 << 18)
+    lim = min((2**31 - 1) // (top_k * max(2 * I, H) * 2), (0x7FFFFFF0 - 1) // (H * 2), 1 << 18)
     return max(lim, 1)
 
 

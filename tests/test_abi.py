@@ -170,13 +170,16 @@ def test_int4_layout_validation_runs_on_the_host():
 
 
 def test_token_chunks_cover_calls_within_the_32bit_bounds():
-    """Layers above one call's addressing bound (T*k*max(H, I)*4 < 2^31) are split into
-    even token chunks: C5's 32768 tokens at top-8, H 2048 become two calls of 16384."""
+    """Layers above one call's addressing bound (T*k*max(2I, H)*2 < 2^31) are split into
+    even token chunks: C5's 32768 tokens at top-8, H 2048, I 1024 are one call; 131072 tokens
+    would be three."""
     from llada_quant_amd.runtime.fused_moe import _chunks, max_tokens_per_call
 
     lim = max_tokens_per_call(2048, 1024, 8)
-    assert lim == (2**31 - 1) // (8 * 2048 * 4) == 32767
-    assert _chunks(32768, lim) == [(0, 16384), (16384, 32768)]
+    assert lim == (2**31 - 1) // (8 * 2048 * 2) == 65535
+    assert _chunks(32768, lim) == [(0, 32768)]
+    assert _chunks(131072, lim) == [(0, 43690), (43690, 87381), (87381, 131072)]
+    assert max_tokens_per_call(1024, 4096, 8) == (2**31 - 1) // (8 * 8192 * 2)  # 2I above H
     for T, lim in [(1, 5), (10, 3), (17, 17), (18, 17), (1000, 7)]:
         spans = _chunks(T, lim)
         assert spans[0][0] == 0 and spans[-1][1] == T
