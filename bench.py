@@ -459,7 +459,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (got --gpus {args.gpus}, "
-              f"WORLD_SIZE={world}); the expert-parallel sharding design is described in DESIGN.md",
+              f"WORLD_SIZE={world}); the path would shard by expert, and one GPU's share is what runs here",
               file=sys.stderr)
         sys.exit(2)
 
