@@ -78,7 +78,7 @@ constexpr int kStageBytes = kRowsMax * kRowBytes;  // one LDS stage
 constexpr int kStages = 2;                      // LDS stages (double buffer)
 constexpr int kF1 = 64;                         // G1 features per item (128 weight rows)
 constexpr int kR2 = 128;                        // G2 output rows per item
-constexpr int kCombineBlock = 256;             // combine: 2 outputs per thread
+constexpr int kCombineBlock = 256;             // combine: threads per workgroup
 
 // 128-wide K chunks of weights in flight per wave: 8 KB per wave either way
 // (INT4: 2 tiles x 1 KB per chunk; INT8: 2 tiles x 2 KB)
@@ -561,49 +561,66 @@ __device__ __forceinline__ void gemm_dispatch(const MoeArgs &a, int e, int slice
     gemm_item<BITS, FOLDED, 2, FIRST, G128>(a, e, slice, row0, rows, ks, lds);
 }
 
-// out[t, h..h+2) = bf16(sum_j y[t*k + j, h..h+2)) over the routed slots, j
-// ascending, summed in fp32 (2 outputs per thread: enough threads to cover
-// every CU).  BF: the slot outputs are bf16 (MoE layers), else fp32
-// (QuantLinear's K-slice partial sums).  The slot ids and slot outputs of a
-// run of 8 slots are loaded together -- one memory round trip -- and the
-// outputs of slots whose id is out of range (never written) are left out of
-// the sum.
+// out[t, h..h+V) = bf16(sum_j y[t*k + j, h..h+V)) over the routed slots, j
+// ascending, summed in fp32.  BF: the slot outputs are bf16 (MoE layers),
+// V = 8 outputs per thread (one 16-byte load per slot); else fp32
+// (QuantLinear's K-slice partial sums), V = 2.  The slot ids and slot
+// outputs of a run of 8 slots are loaded together -- one memory round trip --
+// and the outputs of slots whose id is out of range (never written) are left
+// out of the sum.
 template <bool BF>
 __global__ __launch_bounds__(kCombineBlock) void combine_kernel(const void *__restrict__ ybuf,
                                                                 const int32_t *__restrict__ ids, int64_t T,
                                                                 int H, int k, int E, uint16_t *__restrict__ out) {
-  const int64_t base = (static_cast<int64_t>(blockIdx.x) * kCombineBlock + threadIdx.x) * 2;
-  if (base >= T * H) return;
+  constexpr int V = BF ? 8 : 2;
+  const int64_t base = (static_cast<int64_t>(blockIdx.x) * kCombineBlock + threadIdx.x) * V;
+  if (base >= T * H) return;  // H % V == 0 (H % 128 == 0), so a thread's outputs share one row
   const int64_t t = base / H;
   const int h = static_cast<int>(base - t * H);
   const int32_t *idr = ids + t * k;
-  const int64_t y0 = t * k * H + h;  // element offset of slot 0's pair
-  float s0 = 0.0f, s1 = 0.0f;
+  const int64_t y0 = t * k * H + h;  // element offset of slot 0's outputs
+  float acc[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) acc[v] = 0.0f;
   for (int j0 = 0; j0 < k; j0 += 8) {
     int id[8];
-    float2 v[8];
+    float y[8][V];
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj) {
       const int j = j0 + jj < k ? j0 + jj : k - 1;
       id[jj] = idr[j];
       const int64_t off = y0 + static_cast<int64_t>(j) * H;
       if constexpr (BF) {
-        const uint32_t p = *reinterpret_cast<const uint32_t *>(static_cast<const uint16_t *>(ybuf) + off);
-        v[jj] = make_float2(__uint_as_float(p << 16), __uint_as_float(p & 0xFFFF0000u));
+        const uint4 p = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(ybuf) + off);
+        const uint32_t w[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          y[jj][2 * q] = __uint_as_float(w[q] << 16);
+          y[jj][2 * q + 1] = __uint_as_float(w[q] & 0xFFFF0000u);
+        }
       } else {
-        v[jj] = *reinterpret_cast<const float2 *>(static_cast<const float *>(ybuf) + off);
+        const float2 p = *reinterpret_cast<const float2 *>(static_cast<const float *>(ybuf) + off);
+        y[jj][0] = p.x;
+        y[jj][1] = p.y;
       }
     }
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj) {
       if (j0 + jj < k && id[jj] >= 0 && id[jj] < E) {
-        s0 += v[jj].x;
-        s1 += v[jj].y;
+#pragma unroll
+        for (int v = 0; v < V; ++v) acc[v] += y[jj][v];
       }
     }
   }
-  *reinterpret_cast<uint32_t *>(out + base) =
-      static_cast<uint32_t>(f32_to_bf16_bits(s0)) | (static_cast<uint32_t>(f32_to_bf16_bits(s1)) << 16);
+  uint32_t o[V / 2];
+#pragma unroll
+  for (int q = 0; q < V / 2; ++q)
+    o[q] = static_cast<uint32_t>(f32_to_bf16_bits(acc[2 * q])) |
+           (static_cast<uint32_t>(f32_to_bf16_bits(acc[2 * q + 1])) << 16);
+  if constexpr (BF)
+    *reinterpret_cast<uint4 *>(out + base) = make_uint4(o[0], o[1], o[2], o[3]);
+  else
+    *reinterpret_cast<uint32_t *>(out + base) = o[0];
 }
 
 // Persistent G1 (FIRST) or G2 kernel.  Items are (row block, slice) pairs,
@@ -2849,8 +2866,8 @@ int launch_phases(const MoeArgs &a, int64_t max_g1, int64_t max_g2, hipStream_t 
     int rc = launch_general<BITS, FOLDED>(a, max_g1, max_g2, st, pm, first);
     if (rc) return rc;
   }
-  const int64_t n2 = a.T * a.H / 2;
-  combine_kernel<true><<<static_cast<int>(ceil_div(n2, kCombineBlock)), kCombineBlock, 0, st>>>(a.ybf, a.ids, a.T,
+  const int64_t n8 = a.T * a.H / 8;  // 8 outputs per thread
+  combine_kernel<true><<<static_cast<int>(ceil_div(n8, kCombineBlock)), kCombineBlock, 0, st>>>(a.ybf, a.ids, a.T,
                                                                                                 a.H, a.k, a.E, a.out);
   const int rc = check_launch("moe_combine");
   if (rc) return rc;
