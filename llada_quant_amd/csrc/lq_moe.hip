@@ -748,6 +748,9 @@ __device__ __forceinline__ void wide_chunk(const WChunk<BITS> (&w)[NT], const fl
   uint4 a0[NRT], a1[NRT], b0[NT], b1[NT];
   afrag(0, a0);
   bfrag(0, b0);
+  // every step-0 A read goes out before step 0's interleaved schedule (which
+  // would otherwise place them one by one just ahead of their MFMAs)
+  __builtin_amdgcn_sched_barrier(0);
   step(0, a0, b0, a1, b1);
   step(1, a1, b1, a0, b0);
   step(2, a0, b0, a1, b1);
