@@ -197,7 +197,9 @@ int lq_moe_status(const void *workspace, uint32_t *status, int clear,
 
 /*
  * The quantized expert layer (fused_moe with packed weights):
- *   out[t] = sum_j w[t,j] * W2[e]^T act(W1[e] x[t]),  e = ids[t,j]
+ *   out[t] = bf16(sum_j y[t,j]) (fp32 sum, j ascending),  e = ids[t,j]
+ *   y[t,j] = bf16(w[t,j] * W2[e]^T act(W1[e] x[t])) (the slot output, stored
+ *   in the compute dtype as the Triton fused_moe stores its GEMM2 tiles)
  *   act(g, u) = bf16(bf16(silu(bf16(g))) * bf16(u)), gate = W1[e][:I],
  *   up = W1[e][I:].
  * Replaces dequantize-then-fused_moe: runtime/moe.py:199-216 feeding
@@ -220,7 +222,9 @@ int lq_moe_status(const void *workspace, uint32_t *status, int clear,
  *           contribute nothing
  *   workspace of ws_bytes >= lq_moe_workspace_bytes(T, H, I, E, k)
  * Requires H % 128 == 0, I % 64 == 0, group lengths (after the per-row
- * fallback) that are multiples of 32, and T <= 262144.  Kernels on `stream`:
+ * fallback) that are multiples of 32, T <= 262144 and T*k*max(2I, H)*2 <
+ * 2^31 (the bf16 per-assignment buffers; larger inputs go in token chunks,
+ * which is exact).  Kernels on `stream`:
  * the expert plan, GEMM1, GEMM2, combine, with an x permute in front for the
  * general and wide GEMMs.  With LQ_MOE_FUSED_LAYER, small layers of the
  * streaming family (E <= 64, T*k <= 2048, exact weights) run as ONE launch
