@@ -246,12 +246,23 @@ struct WChunk<8> {
 // such a chunk (it needs group lengths that are multiples of 128).
 // afrag(rt, s): this lane's A fragment (8 bf16 of row rt*16 + lc, K piece
 // 4*lg + s of the chunk, K-slot order) from LDS
-template <int BITS, bool FOLDED, bool FAST, int NRT, int NT, class AFrag>
+// AHEAD: every A fragment of the chunk is read first, so each step's MFMAs
+// find theirs in registers instead of waiting on a read issued just ahead of
+// them (same arithmetic in the same order; 16 * NRT more registers)
+template <int BITS, bool FOLDED, bool FAST, int NRT, int NT, bool AHEAD = false, class AFrag>
 __device__ __forceinline__ void chunk_mfma_f(const WChunk<BITS> (&w)[NT], const float (&sc)[NT], AFrag afrag,
                                              floatx4 (&tot)[NRT][NT]) {
   const uint4 ones4 = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);  // bf16 1.0
   floatx4 acc[NRT][NT];
   floatx4 xs[NRT];
+  uint4 afr[AHEAD ? 4 : 1][NRT];
+  if constexpr (AHEAD) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int rt = 0; rt < NRT; ++rt) afr[s][rt] = afrag(rt, s);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   DqScale dqs[NT];
 #pragma unroll
   for (int c = 0; c < NT; ++c) dqs[c] = dq_scale<BITS>(sc[c]);
@@ -278,7 +289,7 @@ __device__ __forceinline__ void chunk_mfma_f(const WChunk<BITS> (&w)[NT], const 
     }
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt) {
-      const uint4 af = afrag(rt, s);
+      const uint4 af = AHEAD ? afr[AHEAD ? s : 0][rt] : afrag(rt, s);
       if constexpr (!FOLDED) {
 #pragma unroll
         for (int c = 0; c < NT; ++c)
@@ -1532,13 +1543,15 @@ __device__ __forceinline__ void stream_units(const MoeArgs &a, int e, int row0, 
         // chunk cc + d (cc is a multiple of 4): component d % 4 of lane (r, (cc + d) / 4)
         sb[d][0] = __int_as_float(__builtin_amdgcn_ds_bpermute(sqa + 64 * (d >> 2), static_cast<int>(sq_cur[d & 3])));
       }
+      // (the registers of the fused layer kernel and of the folded form do
+      // not hold the chunk's A fragments ahead)
       if constexpr (FOLDED) {
         chunk_mfma_f<BITS, FOLDED, true, NRT, 1>(wb[d], sb[d], afrag, tot);
       } else {
         if (SQ ? fast_unit : __all(dq_fast_ok(sb[d][0])) != 0)
-          chunk_mfma_f<BITS, FOLDED, true, NRT, 1>(wb[d], sb[d], afrag, tot);
+          chunk_mfma_f<BITS, FOLDED, true, NRT, 1, !COH>(wb[d], sb[d], afrag, tot);
         else
-          chunk_mfma_f<BITS, FOLDED, false, NRT, 1>(wb[d], sb[d], afrag, tot);
+          chunk_mfma_f<BITS, FOLDED, false, NRT, 1, !COH>(wb[d], sb[d], afrag, tot);
       }
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (SQ) {
