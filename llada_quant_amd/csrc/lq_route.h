@@ -120,25 +120,40 @@ __device__ __forceinline__ void route_values(const float (&v)[EPL], int E, int k
   }
 }
 
-// Route token t of logits [T, E] (dtype LDT) with one wavefront: writes its k
-// ids and weights to slots t*k .. t*k + k-1 of ids / weights, and the ids also
-// to ids_lds when it is not null (route_values).
+// Token t's logits of [T, E] (dtype LDT) in the lane layout of route_values
+// (lane l holds experts l, l+64, ...; -inf past E).
 template <int LDT, int EPL>
-__device__ __forceinline__ void route_token(const void *__restrict__ logits, int64_t t, int E, int k, int renorm,
-                                            int32_t *__restrict__ ids, float *__restrict__ weights,
-                                            int32_t *ids_lds) {
+__device__ __forceinline__ void route_logits(const void *__restrict__ logits, int64_t t, int E, float (&v)[EPL]) {
   const int lane = threadIdx.x & 63;
-  float v[EPL];
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
     const int e = lane + 64 * j;
     v[j] = e < E ? load_f32<LDT>(logits, t * E + e) : -__builtin_inff();
   }
+}
+
+// Route token t from its logits v (route_logits) with one wavefront: writes
+// its k ids and weights to slots t*k .. t*k + k-1 of ids / weights, and the
+// ids also to ids_lds when it is not null (route_values).
+template <int EPL>
+__device__ __forceinline__ void route_store(const float (&v)[EPL], int64_t t, int E, int k, int renorm,
+                                            int32_t *__restrict__ ids, float *__restrict__ weights,
+                                            int32_t *ids_lds) {
   route_values<EPL>(v, E, k, renorm, [&](int rank, int e, float w) __attribute__((always_inline)) {
     ids[t * k + rank] = e;
     weights[t * k + rank] = w;
     if (ids_lds) ids_lds[t * k + rank] = e;
   });
+}
+
+// route_logits then route_store
+template <int LDT, int EPL>
+__device__ __forceinline__ void route_token(const void *__restrict__ logits, int64_t t, int E, int k, int renorm,
+                                            int32_t *__restrict__ ids, float *__restrict__ weights,
+                                            int32_t *ids_lds) {
+  float v[EPL];
+  route_logits<LDT, EPL>(logits, t, E, v);
+  route_store<EPL>(v, t, E, k, renorm, ids, weights, ids_lds);
 }
 
 // Stable expert permutation (the plan kernel of lq_moe.hip without its work

@@ -14,10 +14,13 @@ namespace lq {
 namespace {
 
 constexpr int kRouteBlock = 256;  // 4 tokens per block, one wave each
+constexpr int kRouteRowRegs = 8;  // 16-byte pieces of x a lane holds: rows up to 8 * 64 * 8 = 4096 wide
 
 // One wavefront per token (route_token).  With xperm != nullptr the wave
 // also copies its token's row of x into xperm in the MoE kernel's K-slot
-// order.
+// order.  Rows up to 4096 wide are read into registers before the routing,
+// so their loads overlap the logits load and the top-k instead of following
+// it one round trip per 1 KB; wider rows are copied afterwards in a loop.
 template <int LDT, int EPL>
 __global__ __launch_bounds__(kRouteBlock) void route_topk_kernel(const void *__restrict__ logits, int64_t T,
                                                                  int E, int k, int renorm,
@@ -26,13 +29,35 @@ __global__ __launch_bounds__(kRouteBlock) void route_topk_kernel(const void *__r
                                                                  const uint16_t *__restrict__ x, int H,
                                                                  uint16_t *__restrict__ xperm) {
   const int lane = threadIdx.x & 63;
-  const int64_t t = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
+  // the wave's token, uniform (a scalar) so the row's buffer descriptor is too
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * (kRouteBlock / 64) +
+                    __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   if (t >= T) return;  // uniform per wave; no block-wide barrier below
-  route_token<LDT, EPL>(logits, t, E, k, renorm, ids, weights, nullptr);
+  float v[EPL];
+  route_logits<LDT, EPL>(logits, t, E, v);  // first, so the routing waits on it alone
+  const int nc = H >> 3;                    // 16-byte pieces per row
+  const bool held = xperm != nullptr && nc <= 64 * kRouteRowRegs;
+  // bounded to the row (to nothing when the row is not held): pieces past H
+  // read zeros without touching memory and are never stored.  No branch, so
+  // the routing's wait covers the logits load alone.
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t *>(held ? x + t * H : x), 0, held ? H * 2 : 0, 0x00020000);
+  uint4 row[kRouteRowRegs];
+#pragma unroll
+  for (int i = 0; i < kRouteRowRegs; ++i)
+    row[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, (lane + 64 * i) * 16, 0, 0));
+  __builtin_amdgcn_sched_barrier(0);  // keeps the row loads ahead of the routing's wait
+  route_store<EPL>(v, t, E, k, renorm, ids, weights, nullptr);
   if (xperm != nullptr) {
-    const uint4 *src = reinterpret_cast<const uint4 *>(x + t * H);
     uint4 *dst = reinterpret_cast<uint4 *>(xperm + t * H);
-    for (int c = lane; c < (H >> 3); c += 64) dst[c] = permute_kslots(src[c]);
+    if (held) {
+#pragma unroll
+      for (int i = 0; i < kRouteRowRegs; ++i)
+        if (lane + 64 * i < nc) dst[lane + 64 * i] = permute_kslots(row[i]);
+    } else {
+      const uint4 *src = reinterpret_cast<const uint4 *>(x + t * H);
+      for (int c = lane; c < nc; c += 64) dst[c] = permute_kslots(src[c]);
+    }
   }
 }
 
