@@ -56,8 +56,8 @@ CONFIGS = {
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=200)
-    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--steps", type=int, default=1000)
+    p.add_argument("--warmup", type=int, default=200)
     p.add_argument("--config", choices=sorted(CONFIGS) + ["c5", "linear"], default="c4")
     p.add_argument("--layers", type=int, default=16, help="c5: layers in the stack")
     p.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0: enough to exceed 3x the MALL)")
